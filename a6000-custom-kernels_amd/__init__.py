@@ -1,0 +1,319 @@
+"""MI355X (gfx950) pointer-table quantized MoE expert GEMV -- Python host mirror.
+
+Thin ctypes bindings over the C ABI in include/ggml_hip_moe_cache.h (the
+library built by build.py), mirroring the reference's operator interface
+(kernels/moe-cache.cuh:15-40): enabled / wants / mul_mat_vec_q / step /
+active / pin_host, plus the activation quantizers and introspection.
+
+The HIP library is the only compute path.  Loading fails loudly when it has
+not been built, and the GEMV/quantizer wrappers refuse non-GPU tensors.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "lib" / "libggml_hip_moe_cache.so"
+
+# ggml_type numbering (ggml.h)
+F32, Q4_0, Q5_0, Q8_0, Q8_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K = 0, 2, 6, 8, 9, 10, 11, 12, 13, 14, 15
+WEIGHT_TYPES = (Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K)
+KQUANTS = (Q2_K, Q3_K, Q4_K, Q5_K, Q6_K)
+BLOCK = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q8_1: (32, 36), Q2_K: (256, 84), Q3_K: (256, 110),
+         Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_K: (256, 292)}
+TYPE_NAMES = {Q4_0: "q4_0", Q5_0: "q5_0", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_K", Q4_K: "q4_K",
+              Q5_K: "q5_K", Q6_K: "q6_K", Q8_1: "q8_1", Q8_K: "q8_K"}
+
+# GLU ops
+GLU_REGLU, GLU_GEGLU, GLU_SWIGLU, GLU_SWIGLU_OAI, GLU_GEGLU_ERF, GLU_GEGLU_QUICK, GLU_SWIGLU_CLAMP = range(7)
+# activation formats
+ACT_Q8_1, ACT_Q8_K = 0, 1
+
+MISS_CAP = 8190
+STATS_WORDS = 2 + MISS_CAP
+
+
+def row_bytes(t: int, k: int) -> int:
+    be, bb = BLOCK[t]
+    assert k % be == 0, (t, k)
+    return k // be * bb
+
+
+class Tensor(C.Structure):
+    """ggml_hip_moe_tensor: POD mirror of the ggml_tensor fields the path reads."""
+    _fields_ = [("type", C.c_int32), ("ne", C.c_int64 * 4), ("nb", C.c_uint64 * 4), ("data", C.c_void_p),
+                ("name", C.c_char_p), ("has_buffer", C.c_int32), ("is_view", C.c_int32)]
+
+
+class Fusion(C.Structure):
+    """ggml_hip_moe_fusion: mirror of ggml_cuda_mm_fusion_args_device (+ explicit extensions)."""
+    _fields_ = [("gate", C.c_void_p), ("x_bias", C.c_void_p), ("gate_bias", C.c_void_p),
+                ("x_scale", C.c_void_p), ("gate_scale", C.c_void_p), ("glu_op", C.c_int32),
+                ("glu_limit", C.c_float), ("shared_up", C.c_void_p), ("shared_gate", C.c_void_p),
+                ("shared_dst", C.c_void_p), ("shared_stride_col_dst", C.c_int64), ("shared_type", C.c_int32),
+                ("shared_src1", C.c_void_p), ("shared_stride_col_y", C.c_int64), ("bias_stride", C.c_int64)]
+
+
+class Config(C.Structure):
+    _fields_ = [("enabled", C.c_int32), ("slots", C.c_int32), ("budget_gb", C.c_double), ("margin_gb", C.c_double),
+                ("seed_path", C.c_char_p), ("max_promotions", C.c_int32), ("verbose", C.c_int32)]
+
+
+class EntryInfo(C.Structure):
+    _fields_ = [("id", C.c_int32), ("type", C.c_int32), ("n_experts", C.c_int32), ("n_slots", C.c_int32),
+                ("expert_bytes", C.c_uint64), ("n_resident", C.c_int32), ("stamps_clock", C.c_uint32)]
+
+
+class Totals(C.Structure):
+    _fields_ = [("steps", C.c_uint64), ("hits", C.c_uint64), ("misses", C.c_uint64), ("promotions", C.c_uint64),
+                ("evictions", C.c_uint64), ("clock", C.c_uint32), ("last_step_misses", C.c_uint32),
+                ("last_step_hits", C.c_uint32), ("admission_size", C.c_uint32)]
+
+
+# (name, restype, argtypes) of every function in include/ggml_hip_moe_cache.h
+_I64, _VP, _I32 = C.c_int64, C.c_void_p, C.c_int32
+_GEMV_TAIL = [_I64] * 4 + [_I64] * 4 + [_I64] * 2 + [_I64] * 4 + [_I64, _VP]
+SIGNATURES = [
+    ("ggml_hip_moe_cache_enabled", C.c_int, []),
+    ("ggml_hip_moe_cache_wants", C.c_int, [C.POINTER(Tensor)]),
+    ("ggml_hip_moe_cache_mul_mat_vec_q", C.c_int,
+     [C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Fusion), _VP, _VP, _VP] + _GEMV_TAIL),
+    ("ggml_hip_moe_cache_step", C.c_int, [_VP]),
+    ("ggml_hip_moe_cache_active", C.c_int, []),
+    ("ggml_hip_moe_cache_pin_host", C.c_int, [C.POINTER(Tensor)]),
+    ("ggml_hip_mul_mat_vec_q_moe", C.c_int, [C.POINTER(Tensor), C.POINTER(Fusion), _VP, _VP, _VP] + _GEMV_TAIL),
+    ("ggml_hip_moe_mul_mat_vec_ex", C.c_int,
+     [C.c_int, C.c_int, C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Fusion), _VP, _VP, _VP]
+     + [_I64] * 3 + [_I64] * 3 + [_I64] * 4 + [_I64, _VP]),
+    ("ggml_hip_quantize_q8_1", C.c_int, [_VP, _VP, _I64, _I64, _I64, _I64, _VP]),
+    ("ggml_hip_quantize_q8_K", C.c_int, [_VP, _VP, _I64, _I64, _I64, _I64, _VP]),
+    ("ggml_hip_quantize_q8_0_as_q8_1", C.c_int, [_VP, _VP, _I64, _I64, _I64, _I64, _VP]),
+    ("ggml_hip_moe_cache_configure", C.c_int, [C.POINTER(Config)]),
+    ("ggml_hip_moe_cache_get_config", C.c_int, [C.POINTER(Config)]),
+    ("ggml_hip_moe_cache_num_entries", C.c_int, []),
+    ("ggml_hip_moe_cache_entry_info", C.c_int, [_I32, C.POINTER(EntryInfo)]),
+    ("ggml_hip_moe_cache_entry_slots", C.c_int, [_I32, _VP, _I32, _VP, _I32]),
+    ("ggml_hip_moe_cache_entry_table", C.c_int, [_I32, _VP, _I32]),
+    ("ggml_hip_moe_cache_entry_device", C.c_int, [_I32, C.POINTER(_VP), C.POINTER(_VP), C.POINTER(_VP)]),
+    ("ggml_hip_moe_cache_device_globals", C.c_int, [C.POINTER(_VP), C.POINTER(_VP)]),
+    ("ggml_hip_moe_cache_stats_snapshot", C.c_int, [_VP, _I32, _VP]),
+    ("ggml_hip_moe_cache_stamps_snapshot", C.c_int, [_I32, _VP, _I32, _VP]),
+    ("ggml_hip_moe_cache_totals", C.c_int, [C.POINTER(Totals)]),
+    ("ggml_hip_moe_cache_reset", C.c_int, []),
+    ("ggml_hip_moe_last_error", C.c_char_p, []),
+    ("ggml_hip_moe_version", C.c_char_p, []),
+]
+
+
+class MoeError(RuntimeError):
+    pass
+
+
+def bind(path) -> C.CDLL:
+    lib = C.CDLL(str(path))
+    for name, res, args in SIGNATURES:
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = res, args
+    return lib
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """The gfx950 library; raises if it has not been built (no fallback exists)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise MoeError(f"{LIB_PATH} is missing: build it with `python a6000-custom-kernels_amd/build.py` "
+                           "(or __graft_entry__.build()); there is no CPU fallback")
+        _lib = bind(LIB_PATH)
+    return _lib
+
+
+def check(rc: int, what: str = "") -> int:
+    if rc < 0:
+        msg = lib().ggml_hip_moe_last_error().decode(errors="replace")
+        raise MoeError(f"{what}: {msg} (rc={rc})")
+    return rc
+
+
+def make_tensor(wtype: int, ne00: int, ne01: int, ne02: int, data_ptr: int, name: str = "",
+                has_buffer: bool = True, is_view: bool = False, keep: list | None = None) -> Tensor:
+    t = Tensor()
+    rb = row_bytes(wtype, ne00)
+    t.type = wtype
+    t.ne[:] = [ne00, ne01, ne02, 1]
+    t.nb[:] = [BLOCK[wtype][1], rb, rb * ne01, rb * ne01 * ne02]
+    t.data = data_ptr
+    nm = name.encode()
+    t.name = nm
+    if keep is not None:
+        keep.append(nm)
+    t.has_buffer = 1 if has_buffer else 0
+    t.is_view = 1 if is_view else 0
+    return t
+
+
+# ---------------------------------------------------------------------------
+# torch-facing helpers (device memory + streams are torch's)
+# ---------------------------------------------------------------------------
+
+def _torch():
+    import torch
+    return torch
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream=None):
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+def _require_gpu(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise MoeError("HIP path requires device tensors (no CPU fallback)")
+
+
+def quantize_q8_1(x, out=None, stream=None, kind: str = "q8_1"):
+    """x: float32 [rows, k] on the GPU -> uint8 [rows, k/32*36] (q8_1 layout)."""
+    torch = _torch()
+    _require_gpu(x)
+    assert x.dtype == torch.float32 and x.dim() == 2 and x.stride(1) == 1
+    rows, k = x.shape
+    if out is None:
+        out = torch.empty((rows, k // 32 * 36), dtype=torch.uint8, device=x.device)
+    fn = lib().ggml_hip_quantize_q8_1 if kind == "q8_1" else lib().ggml_hip_quantize_q8_0_as_q8_1
+    check(fn(x.data_ptr(), out.data_ptr(), k, rows, x.stride(0), out.stride(0) // 36, _stream(stream)), "quantize_q8_1")
+    return out
+
+
+def quantize_q8_K(x, out=None, stream=None):
+    torch = _torch()
+    _require_gpu(x)
+    assert x.dtype == torch.float32 and x.dim() == 2 and x.stride(1) == 1
+    rows, k = x.shape
+    if out is None:
+        out = torch.empty((rows, k // 256 * 292), dtype=torch.uint8, device=x.device)
+    check(lib().ggml_hip_quantize_q8_K(x.data_ptr(), out.data_ptr(), k, rows, x.stride(0), out.stride(0) // 292,
+                                       _stream(stream)), "quantize_q8_K")
+    return out
+
+
+def make_fusion(*, gate=None, x_bias=None, gate_bias=None, x_scale=None, gate_scale=None, glu_op=GLU_SWIGLU,
+                glu_limit=0.0, shared_up=None, shared_gate=None, shared_dst=None, shared_type=-1,
+                shared_src1=None, shared_stride_col_y=0, bias_stride=0) -> Fusion:
+    f = Fusion()
+    f.gate = _ptr(gate)
+    f.x_bias, f.gate_bias = _ptr(x_bias), _ptr(gate_bias)
+    f.x_scale, f.gate_scale = _ptr(x_scale), _ptr(gate_scale)
+    f.glu_op, f.glu_limit = glu_op, glu_limit
+    f.shared_up, f.shared_gate, f.shared_dst = _ptr(shared_up), _ptr(shared_gate), _ptr(shared_dst)
+    f.shared_stride_col_dst = shared_dst.shape[-1] if shared_dst is not None else 0
+    f.shared_type = shared_type
+    f.shared_src1 = _ptr(shared_src1)
+    f.shared_stride_col_y = shared_stride_col_y
+    f.bias_stride = bias_stride
+    return f
+
+
+def mul_mat_vec(*, wtype, weights, ids, y, dst, K, R, n_experts, use_cache=False, act=ACT_Q8_1, gate_host=None,
+                fusion: Fusion | None = None, nchannels_y=1, name="", stream=None, weights_ptr=None, gate_ptr=None):
+    """Run the GEMV through ggml_hip_moe_mul_mat_vec_ex.
+
+    weights: device uint8 tensor [n_experts, R, row_bytes] (use_cache=False) or a pinned host pointer
+    (weights_ptr, use_cache=True); ids: int32 [n_tok, n_used] (device); y: activation blocks,
+    [n_tok, nchannels_y, act_row_bytes] (device); dst: float32 [n_tok, n_used, R] (device).
+    """
+    n_tok, n_used = ids.shape
+    _require_gpu(ids, y, dst)
+    keep = []
+    ptr = weights_ptr if weights_ptr is not None else weights.data_ptr()
+    src0 = make_tensor(wtype, K, R, n_experts, ptr, name=name, keep=keep)
+    g = None
+    if gate_ptr is not None:
+        g = make_tensor(wtype, K, R, n_experts, gate_ptr, name=name.replace("up", "gate"), keep=keep)
+    ablk = (32, 36) if act == ACT_Q8_1 else (256, 292)
+    act_row = K // ablk[0]
+    rc = lib().ggml_hip_moe_mul_mat_vec_ex(
+        1 if use_cache else 0, act, C.byref(src0), C.byref(g) if g is not None else None,
+        C.byref(fusion) if fusion is not None else None, y.data_ptr(), ids.data_ptr(), dst.data_ptr(),
+        K, R, n_experts, n_tok, nchannels_y, n_used,
+        nchannels_y * act_row, n_used * R, act_row, R, ids.stride(0), _stream(stream))
+    check(rc, "mul_mat_vec")
+    return dst
+
+
+def configure(*, enabled=True, slots=-1, budget_gb=0.0, margin_gb=2.0, seed_path=None, max_promotions=48,
+              verbose=False):
+    cfg = Config()
+    cfg.enabled, cfg.slots, cfg.budget_gb, cfg.margin_gb = int(enabled), slots, budget_gb, margin_gb
+    cfg._seed = seed_path.encode() if seed_path else None
+    cfg.seed_path = cfg._seed
+    cfg.max_promotions, cfg.verbose = max_promotions, int(verbose)
+    check(lib().ggml_hip_moe_cache_configure(C.byref(cfg)), "configure")
+
+
+def reset():
+    check(lib().ggml_hip_moe_cache_reset(), "reset")
+
+
+def step(stream=None):
+    return check(lib().ggml_hip_moe_cache_step(_stream(stream)), "step")
+
+
+def entry_info(i: int) -> EntryInfo:
+    info = EntryInfo()
+    check(lib().ggml_hip_moe_cache_entry_info(i, C.byref(info)), "entry_info")
+    return info
+
+
+def entry_state(i: int):
+    import numpy as np
+    info = entry_info(i)
+    slot_of = np.empty(info.n_experts, dtype=np.int32)
+    expert_of = np.empty(max(info.n_slots, 1), dtype=np.int32)
+    table = np.empty(info.n_experts, dtype=np.int32)
+    check(lib().ggml_hip_moe_cache_entry_slots(i, slot_of.ctypes.data, info.n_experts, expert_of.ctypes.data,
+                                               info.n_slots), "entry_slots")
+    check(lib().ggml_hip_moe_cache_entry_table(i, table.ctypes.data, info.n_experts), "entry_table")
+    return {"info": info, "slot_of": slot_of, "expert_of": expert_of[:info.n_slots], "table": table}
+
+
+def totals() -> Totals:
+    t = Totals()
+    check(lib().ggml_hip_moe_cache_totals(C.byref(t)), "totals")
+    return t
+
+
+def device_globals():
+    s, c = C.c_void_p(), C.c_void_p()
+    check(lib().ggml_hip_moe_cache_device_globals(C.byref(s), C.byref(c)), "device_globals")
+    return s.value, c.value
+
+
+def entry_device(i: int):
+    t, s, p = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    check(lib().ggml_hip_moe_cache_entry_device(i, C.byref(t), C.byref(s), C.byref(p)), "entry_device")
+    return t.value, s.value, p.value
+
+
+def stats_snapshot(n_words: int = STATS_WORDS, stream=None):
+    import numpy as np
+    out = np.zeros(n_words, dtype=np.uint32)
+    check(lib().ggml_hip_moe_cache_stats_snapshot(out.ctypes.data, n_words, _stream(stream)), "stats_snapshot")
+    return out
+
+
+def stamps_snapshot(i: int, stream=None):
+    import numpy as np
+    n = entry_info(i).n_experts
+    out = np.zeros(n, dtype=np.uint32)
+    check(lib().ggml_hip_moe_cache_stamps_snapshot(i, out.ctypes.data, n, _stream(stream)), "stamps_snapshot")
+    return out

@@ -1,0 +1,925 @@
+// mc_host.cpp -- host side of the pointer-table MoE GEMV: configuration,
+// per-tensor registration (pointer table, HBM pool, stamps), seed loading,
+// the between-graph LRU promotion step and the C ABI.
+//
+// Restates the host half of kernels/moe-cache.cu (:293-868) for one MI355X:
+//   * pools are sized for 288 GB of HBM3E: by default every expert of a tensor
+//     gets a slot and the budget is whatever hipMemGetInfo reports free minus a
+//     margin (reference: 320 slots, 30 GiB, 2 GiB margin; :317-318, :549-556);
+//   * host expert memory is addressed on the device through
+//     hipHostGetDevicePointer, not the raw host address;
+//   * errors return a status (reference: CUDA_CHECK / GGML_ABORT aborts).
+#include <errno.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/ggml_hip_moe_cache.h"
+#include "mc_device.h"
+#include "mc_internal.h"
+
+namespace mc {
+namespace {
+
+thread_local std::string t_last_error;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    t_last_error = buf;
+    return code;
+}
+
+constexpr int E_INVALID = -1;
+constexpr int E_UNSUPPORTED = -2;
+constexpr int E_DEVICE = -3;
+constexpr int E_DISABLED = -4;
+constexpr int E_STATE = -5;
+
+// ---------------------------------------------------------------------------
+// configuration (kernels/moe-cache.cu:330-363)
+// ---------------------------------------------------------------------------
+
+struct Config {
+    bool enabled = false;
+    int slots = -1;                       // < 0: every expert of the tensor
+    double budget_gb = 0.0;               // <= 0: adaptive (free HBM - margin)
+    double margin_gb = 2.0;
+    std::string seed_path;
+    int max_promotions = DEFAULT_MAX_PROMOTIONS;
+    bool verbose = false;
+    bool debug = false;
+    bool allow_register = false;
+};
+
+Config g_cfg;
+bool g_cfg_ready = false;
+
+const char *env2(const char *hip_name, const char *cuda_name) {
+    const char *v = getenv(hip_name);
+    if (!v && cuda_name) v = getenv(cuda_name);
+    return v;
+}
+
+void read_env_locked() {
+    if (g_cfg_ready) return;
+    Config c;
+    const char *en = env2("GGML_HIP_MOE_CACHE", "GGML_CUDA_MOE_CACHE");
+    c.enabled = en && en[0] && en[0] != '0';
+    if (const char *s = env2("GGML_HIP_MOE_CACHE_SLOTS", "GGML_CUDA_MOE_CACHE_SLOTS")) c.slots = std::max(0, atoi(s));
+    if (const char *s = env2("GGML_HIP_MOE_CACHE_BUDGET_GB", "GGML_CUDA_MOE_CACHE_BUDGET_GB")) {
+        const double gb = atof(s);
+        if (gb > 0) c.budget_gb = gb;
+    }
+    if (const char *s = getenv("GGML_HIP_MOE_CACHE_MARGIN_GB")) c.margin_gb = std::max(0.0, atof(s));
+    if (const char *s = env2("GGML_HIP_MOE_CACHE_SEED", "GGML_CUDA_MOE_CACHE_SEED")) c.seed_path = s;
+    if (const char *s = getenv("GGML_HIP_MOE_CACHE_MAX_PROMOTIONS")) c.max_promotions = std::max(0, atoi(s));
+    c.debug = env2("GGML_HIP_MOE_CACHE_DEBUG", "GGML_CUDA_MOE_CACHE_DEBUG") != nullptr;
+    c.verbose = c.debug || getenv("GGML_HIP_MOE_CACHE_VERBOSE") != nullptr;
+    const char *ar = getenv("GGML_HIP_MOE_CACHE_ALLOW_REGISTER");
+    c.allow_register = ar && ar[0] == '1';
+    g_cfg = c;
+    g_cfg_ready = true;
+    if (g_cfg.enabled && g_cfg.verbose) {
+        fprintf(stderr, "moe-cache: enabled, slots=%d budget=%s margin=%.1f GB\n", g_cfg.slots,
+                g_cfg.budget_gb > 0 ? "fixed" : "adaptive", g_cfg.margin_gb);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// registry state (kernels/moe-cache.cu:297-328)
+// ---------------------------------------------------------------------------
+
+struct Entry {
+    int32_t id = -1;
+    int type = 0;
+    const char *data = nullptr;          // host base of the expert tensor (copy source)
+    uintptr_t dev_base = 0;              // device-visible address of `data`
+    size_t expert_bytes = 0;
+    int n_experts = 0;
+    int n_slots = 0;
+    char *pool = nullptr;                // device, n_slots * expert_bytes
+    uint64_t *d_tbl = nullptr;           // device, tagged pointers
+    std::vector<uint64_t> h_tbl;         // host mirror
+    uint32_t *d_stamps = nullptr;        // device, last-use clock per expert
+    std::vector<int32_t> slot_of;        // expert -> slot (-1: cold)
+    std::vector<int32_t> expert_of;      // slot -> expert (-1: free)
+    std::vector<uint32_t> h_stamps;      // host mirror of d_stamps for eviction
+    uint32_t stamps_clock = 0;           // clock at the last mirror refresh
+    bool tbl_dirty = false;
+    std::string name;
+};
+
+// Table of a device-resident expert tensor (no pool, no stats).
+struct Resident {
+    uint64_t *d_tbl = nullptr;
+    std::vector<uint64_t> h_tbl;
+    int n_experts = 0;
+    int cap = 0;                         // entries d_tbl can hold
+    size_t expert_bytes = 0;
+};
+
+std::mutex g_mutex;                                  // registry + step
+std::unordered_map<const char *, Entry *> g_by_data;
+std::vector<Entry *> g_all;
+std::unordered_map<const void *, Resident *> g_resident;
+uint32_t *g_d_stats = nullptr;                       // device [STATS_WORDS]
+uint32_t *g_h_stats = nullptr;                       // pinned host mirror (+1 word: clock staging)
+uint32_t *g_d_clock = nullptr;
+uint32_t g_h_clock = 0;
+size_t g_used = 0;                                   // pool bytes allocated
+std::unordered_map<uint32_t, int> g_admission;       // (id << 12 | expert) -> sightings
+std::unordered_map<std::string, std::vector<int>> g_seed;
+bool g_seed_loaded = false;
+ggml_hip_moe_totals g_totals = {};
+
+std::unordered_map<const void *, int> g_ptr_kind;    // cached residency test
+std::mutex g_ptr_mutex;
+
+Device *dev() { return default_device(); }
+
+int dev_err(int code, const char *what) {
+    return fail(E_DEVICE, "moe-cache: %s failed on %s: %s (%d)", what, dev()->name(), dev()->error_string(code), code);
+}
+
+int ptr_kind_cached(const void *p) {
+    std::lock_guard<std::mutex> lock(g_ptr_mutex);
+    auto it = g_ptr_kind.find(p);
+    if (it != g_ptr_kind.end()) return it->second;
+    const int k = dev()->ptr_kind(p);
+    g_ptr_kind[p] = k;
+    return k;
+}
+
+bool is_contiguous(const ggml_hip_moe_tensor *t) {
+    const TypeGeom g = type_geom(t->type);
+    if (g.block_elems == 0 || t->ne[0] % g.block_elems) return false;
+    const uint64_t rb = (uint64_t) (t->ne[0] / g.block_elems) * g.block_bytes;
+    return t->nb[0] == (uint64_t) g.block_bytes && t->nb[1] == rb && t->nb[2] == rb * (uint64_t) t->ne[1] &&
+           t->nb[3] == t->nb[2] * (uint64_t) t->ne[2];
+}
+
+int init_globals_locked(void *stream) {
+    if (g_d_stats) return 0;
+    int rc;
+    if ((rc = dev()->malloc_dev((void **) &g_d_stats, sizeof(uint32_t) * STATS_WORDS))) return dev_err(rc, "stats alloc");
+    if ((rc = dev()->malloc_host((void **) &g_h_stats, sizeof(uint32_t) * (STATS_WORDS + 2)))) return dev_err(rc, "pinned stats alloc");
+    if ((rc = dev()->malloc_dev((void **) &g_d_clock, sizeof(uint32_t)))) return dev_err(rc, "clock alloc");
+    memset(g_h_stats, 0, sizeof(uint32_t) * (STATS_WORDS + 2));
+    if ((rc = dev()->memset_dev(g_d_stats, 0, sizeof(uint32_t) * STATS_WORDS, stream))) return dev_err(rc, "stats clear");
+    if ((rc = dev()->memset_dev(g_d_clock, 0, sizeof(uint32_t), stream))) return dev_err(rc, "clock clear");
+    g_h_clock = 0;
+    return 0;
+}
+
+// seed file: lines "tensorname id1,id2,..." (kernels/moe-cache.cu:483-523)
+void load_seed_locked() {
+    if (g_seed_loaded) return;
+    g_seed_loaded = true;
+    const std::string &path = g_cfg.seed_path;
+    if (path.empty()) return;
+    FILE *f = fopen(path.c_str(), "r");
+    if (!f) {
+        if (g_cfg.verbose) fprintf(stderr, "moe-cache: seed file %s not found, starting cold\n", path.c_str());
+        return;
+    }
+    static char line[1 << 16];
+    while (fgets(line, sizeof(line), f)) {
+        char *sp = strchr(line, ' ');
+        if (!sp) continue;
+        *sp = 0;
+        std::vector<int> ids;
+        char *p = sp + 1;
+        while (*p) {
+            char *end = nullptr;
+            const long v = strtol(p, &end, 10);
+            if (end == p) break;
+            ids.push_back((int) v);
+            p = (*end == ',') ? end + 1 : end;
+        }
+        g_seed[line] = std::move(ids);
+    }
+    fclose(f);
+    if (g_cfg.verbose) fprintf(stderr, "moe-cache: loaded seed for %zu tensors from %s\n", g_seed.size(), path.c_str());
+}
+
+uint64_t host_entry(const Entry *e, int expert) {
+    return (uint64_t) (e->dev_base + (uintptr_t) expert * e->expert_bytes) | 1ull;
+}
+uint64_t pool_entry(const Entry *e, int slot) { return (uint64_t) (uintptr_t) (e->pool + (size_t) slot * e->expert_bytes); }
+
+// registration (kernels/moe-cache.cu:525-622)
+int get_or_create_locked(const ggml_hip_moe_tensor *src0, void *stream, Entry **out) {
+    int rc = init_globals_locked(stream);
+    if (rc) return rc;
+    auto it = g_by_data.find((const char *) src0->data);
+    if (it != g_by_data.end()) {
+        *out = it->second;
+        return 0;
+    }
+    void *dbase = nullptr;
+    if ((rc = dev()->host_device_ptr(src0->data, &dbase))) return dev_err(rc, "hipHostGetDevicePointer");
+
+    Entry *e = new Entry();
+    e->id = (int32_t) g_all.size();
+    e->type = src0->type;
+    e->data = (const char *) src0->data;
+    e->dev_base = (uintptr_t) dbase;
+    e->expert_bytes = (size_t) src0->nb[2];
+    e->n_experts = (int) src0->ne[2];
+    e->name = src0->name ? src0->name : "";
+
+    const size_t eb = e->expert_bytes;
+    long long slots = g_cfg.slots < 0 ? (long long) e->n_experts : (long long) g_cfg.slots;
+    if (g_cfg.budget_gb > 0) {
+        const size_t budget = (size_t) (g_cfg.budget_gb * 1024.0 * 1024.0 * 1024.0);
+        const size_t free_budget = budget > g_used ? budget - g_used : 0;
+        if ((size_t) slots * eb > free_budget) slots = (long long) (free_budget / eb);
+    }
+    size_t free_b = 0, total_b = 0;
+    if ((rc = dev()->mem_info(&free_b, &total_b))) {
+        delete e;
+        return dev_err(rc, "hipMemGetInfo");
+    }
+    const size_t margin = (size_t) (g_cfg.margin_gb * 1024.0 * 1024.0 * 1024.0);
+    const size_t usable = free_b > margin ? free_b - margin : 0;
+    if ((size_t) slots * eb > usable) slots = (long long) (usable / eb);
+    if (slots > e->n_experts) slots = e->n_experts;
+    e->n_slots = (int) slots;
+
+    e->h_tbl.resize(e->n_experts);
+    for (int i = 0; i < e->n_experts; ++i) e->h_tbl[i] = host_entry(e, i);
+    if ((rc = dev()->malloc_dev((void **) &e->d_tbl, sizeof(uint64_t) * e->n_experts))) { delete e; return dev_err(rc, "table alloc"); }
+    if ((rc = dev()->malloc_dev((void **) &e->d_stamps, sizeof(uint32_t) * e->n_experts))) {
+        dev()->free_dev(e->d_tbl);
+        delete e;
+        return dev_err(rc, "stamps alloc");
+    }
+    if ((rc = dev()->memset_dev(e->d_stamps, 0, sizeof(uint32_t) * e->n_experts, stream))) return dev_err(rc, "stamps clear");
+    e->h_stamps.assign(e->n_experts, 0);
+    e->slot_of.assign(e->n_experts, -1);
+    e->expert_of.assign(e->n_slots, -1);
+    if (e->n_slots > 0) {
+        if ((rc = dev()->malloc_dev((void **) &e->pool, (size_t) e->n_slots * eb))) {
+            dev()->free_dev(e->d_tbl);
+            dev()->free_dev(e->d_stamps);
+            delete e;
+            return dev_err(rc, "pool alloc");
+        }
+        g_used += (size_t) e->n_slots * eb;
+    }
+    g_by_data[e->data] = e;
+    g_all.push_back(e);
+
+    // seed slots 0..k-1 in seed order, skipping out-of-range and repeated ids
+    load_seed_locked();
+    auto sit = g_seed.find(e->name);
+    int seeded = 0;
+    if (sit != g_seed.end() && e->n_slots > 0) {
+        for (const int expert : sit->second) {
+            if (seeded >= e->n_slots) break;
+            if (expert < 0 || expert >= e->n_experts || e->slot_of[expert] >= 0) continue;
+            const int slot = seeded;
+            if ((rc = dev()->copy_h2d(e->pool + (size_t) slot * eb, e->data + (size_t) expert * eb, eb, stream)))
+                return dev_err(rc, "seed copy");
+            e->h_tbl[expert] = pool_entry(e, slot);
+            e->slot_of[expert] = slot;
+            e->expert_of[slot] = expert;
+            seeded += 1;
+        }
+    }
+    // one upload covers the host entries and every seeded slot, ordered after the copies
+    if ((rc = dev()->copy_h2d(e->d_tbl, e->h_tbl.data(), sizeof(uint64_t) * e->n_experts, stream)))
+        return dev_err(rc, "table upload");
+    if (g_cfg.verbose) {
+        fprintf(stderr, "moe-cache: registered %s type=%d experts=%d slot_bytes=%zu slots=%d seeded=%d (pool %.1f MB, total %.2f GB, free HBM %.2f GB)\n",
+                e->name.empty() ? "<tensor>" : e->name.c_str(), e->type, e->n_experts, eb, e->n_slots, seeded,
+                (double) e->n_slots * eb / (1024.0 * 1024.0), (double) g_used / (1024.0 * 1024.0 * 1024.0),
+                (double) free_b / (1024.0 * 1024.0 * 1024.0));
+    }
+    *out = e;
+    return 0;
+}
+
+// LRU slot acquisition (kernels/moe-cache.cu:628-667)
+int acquire_slot_locked(Entry *e, void *stream, int *slot_out) {
+    *slot_out = -1;
+    if (e->n_slots == 0) return 0;
+    for (int s = 0; s < e->n_slots; ++s) {
+        if (e->expert_of[s] < 0) {
+            *slot_out = s;
+            return 0;
+        }
+    }
+    if (e->stamps_clock != g_h_clock) {
+        int rc;
+        if ((rc = dev()->copy_d2h(e->h_stamps.data(), e->d_stamps, sizeof(uint32_t) * e->n_experts, stream))) return dev_err(rc, "stamps readback");
+        if ((rc = dev()->sync(stream))) return dev_err(rc, "stream sync");
+        e->stamps_clock = g_h_clock;
+    }
+    int victim_slot = -1;
+    uint32_t best = UINT32_MAX;
+    for (int s = 0; s < e->n_slots; ++s) {
+        const int expert = e->expert_of[s];
+        const uint32_t stamp = expert >= 0 ? e->h_stamps[expert] : 0;
+        if (stamp < best) {
+            best = stamp;
+            victim_slot = s;
+        }
+    }
+    if (victim_slot < 0) return 0;
+    const int victim = e->expert_of[victim_slot];
+    if (victim >= 0) {
+        e->slot_of[victim] = -1;
+        e->h_tbl[victim] = host_entry(e, victim);
+        e->tbl_dirty = true;
+        g_totals.evictions += 1;
+    }
+    e->expert_of[victim_slot] = -1;
+    *slot_out = victim_slot;
+    return 0;
+}
+
+// between-graph promotion step (kernels/moe-cache.cu:669-775)
+int step_locked(void *stream) {
+    int rc;
+    if ((rc = dev()->copy_d2h(g_h_stats, g_d_stats, sizeof(uint32_t) * STATS_WORDS, stream))) return dev_err(rc, "stats readback");
+    if ((rc = dev()->sync(stream))) return dev_err(rc, "stream sync");
+    uint32_t n = g_h_stats[0];
+    if (n > (uint32_t) MISS_CAP) n = MISS_CAP;
+    const uint32_t step_hits = g_h_stats[HIT_WORD];
+
+    g_h_clock += 1;
+    g_h_stats[STATS_WORDS] = g_h_clock;          // pinned staging word for the clock upload
+    if ((rc = dev()->copy_h2d(g_d_clock, &g_h_stats[STATS_WORDS], sizeof(uint32_t), stream))) return dev_err(rc, "clock upload");
+    if ((rc = dev()->memset_dev(g_d_stats, 0, 2 * sizeof(uint32_t), stream))) return dev_err(rc, "stats reset");
+
+    g_totals.steps += 1;
+    g_totals.misses += n;
+    g_totals.hits += step_hits;
+    g_totals.clock = g_h_clock;
+    g_totals.last_step_misses = n;
+    g_totals.last_step_hits = step_hits;
+    if (g_cfg.verbose && g_totals.steps % 64 == 0) {
+        size_t resident = 0;
+        for (const Entry *e : g_all)
+            for (int s = 0; s < e->n_slots; ++s) resident += e->expert_of[s] >= 0 ? 1 : 0;
+        fprintf(stderr, "moe-cache: step %llu: hits=%u misses=%u (totals: hits %llu, misses %llu, promos %llu), resident %zu\n",
+                (unsigned long long) g_totals.steps, step_hits, n, (unsigned long long) g_totals.hits,
+                (unsigned long long) g_totals.misses, (unsigned long long) g_totals.promotions, resident);
+    }
+    if (n == 0) return 0;
+
+    // admission: promote on the 2nd sighting; the count resets even when promotion fails
+    int promoted = 0;
+    for (uint32_t i = 0; i < n && promoted < g_cfg.max_promotions; ++i) {
+        const uint32_t packed = g_h_stats[LOG_BASE + i];
+        const int32_t cid = (int32_t) (packed >> 12);
+        const int32_t expert = (int32_t) (packed & 0xFFF);
+        int &count = g_admission[packed];
+        count += 1;
+        if (count < 2) continue;
+        count = 0;
+        if (cid < 0 || cid >= (int32_t) g_all.size()) continue;
+        Entry *e = g_all[cid];
+        if (expert < 0 || expert >= e->n_experts || e->slot_of[expert] >= 0) continue;
+        int slot;
+        if ((rc = acquire_slot_locked(e, stream, &slot))) return rc;
+        if (slot < 0) continue;
+        if ((rc = dev()->copy_h2d(e->pool + (size_t) slot * e->expert_bytes, e->data + (size_t) expert * e->expert_bytes,
+                                  e->expert_bytes, stream)))
+            return dev_err(rc, "promotion copy");
+        e->h_tbl[expert] = pool_entry(e, slot);
+        e->tbl_dirty = true;
+        e->slot_of[expert] = slot;
+        e->expert_of[slot] = expert;
+        promoted += 1;
+        g_totals.promotions += 1;
+    }
+    // one table upload per touched tensor, after the pool copies
+    for (Entry *e : g_all) {
+        if (!e->tbl_dirty) continue;
+        if ((rc = dev()->copy_h2d(e->d_tbl, e->h_tbl.data(), sizeof(uint64_t) * e->n_experts, stream))) return dev_err(rc, "table flush");
+        e->tbl_dirty = false;
+    }
+    if (g_admission.size() > 8192) {
+        for (auto it = g_admission.begin(); it != g_admission.end();) {
+            if (it->second == 0) it = g_admission.erase(it);
+            else ++it;
+        }
+    }
+    g_totals.admission_size = (uint32_t) g_admission.size();
+    return 0;
+}
+
+int resident_table_locked(const void *data, int n_experts, size_t eb, void *stream, Resident **out) {
+    // The table of a device-resident tensor is a pure function of (base, n_experts,
+    // expert_bytes).  Allocators reuse addresses, so a cached table whose shape no
+    // longer matches is rewritten in place (stream-ordered after earlier launches).
+    int rc;
+    Resident *r;
+    auto it = g_resident.find(data);
+    if (it != g_resident.end()) {
+        r = it->second;
+        if (r->n_experts == n_experts && r->expert_bytes == eb) {
+            *out = r;
+            return 0;
+        }
+        // earlier launches and the previous upload (from h_tbl) must be done first
+        if ((rc = dev()->sync(stream))) return dev_err(rc, "stream sync");
+        if (r->cap < n_experts) {
+            if ((rc = dev()->free_dev(r->d_tbl))) return dev_err(rc, "resident table free");
+            r->d_tbl = nullptr;
+        }
+    } else {
+        r = new Resident();
+        g_resident[data] = r;
+    }
+    if (!r->d_tbl) {
+        if ((rc = dev()->malloc_dev((void **) &r->d_tbl, sizeof(uint64_t) * (size_t) n_experts))) {
+            g_resident.erase(data);
+            delete r;
+            return dev_err(rc, "resident table alloc");
+        }
+        r->cap = n_experts;
+    }
+    r->n_experts = n_experts;
+    r->expert_bytes = eb;
+    r->h_tbl.resize(n_experts);
+    for (int i = 0; i < n_experts; ++i) r->h_tbl[i] = (uint64_t) ((uintptr_t) data + (uintptr_t) i * eb);
+    if ((rc = dev()->copy_h2d(r->d_tbl, r->h_tbl.data(), sizeof(uint64_t) * n_experts, stream))) return dev_err(rc, "resident table upload");
+    *out = r;
+    return 0;
+}
+
+bool wants_impl(const ggml_hip_moe_tensor *src0) {
+    {
+        std::lock_guard<std::mutex> lock(g_mutex);
+        read_env_locked();
+        if (!g_cfg.enabled) return false;
+    }
+    if (!src0 || !src0->has_buffer || !src0->data) return false;
+    if (ptr_kind_cached(src0->data) != PTR_HOST) {
+        if (g_cfg.debug && src0->ne[2] > 1)
+            fprintf(stderr, "moe-cache: wants? %s type=%d ne2=%lld ptr=%p: not GPU-readable host memory\n",
+                    src0->name ? src0->name : "<tensor>", src0->type, (long long) src0->ne[2], src0->data);
+        return false;
+    }
+    if (!type_supported(src0->type)) return false;
+    if (src0->ne[2] < 2 || src0->ne[3] != 1 || src0->is_view) return false;
+    return is_contiguous(src0);
+}
+
+// Shared validation + launch of the GEMV.
+int gemv_common(int use_cache, int act, const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *gate_host,
+                const ggml_hip_moe_fusion *fusion, const void *src1, const int32_t *ids_d, float *dst_d,
+                int64_t ne00, int64_t ne01, int64_t ne02, int64_t ncols_dst, int64_t nchannels_y, int64_t nchannels_dst,
+                int64_t stride_col_y, int64_t stride_col_dst, int64_t stride_channel_y, int64_t stride_channel_dst,
+                int64_t ids_stride, void *stream) {
+    if (!src0 || !src1 || !ids_d || !dst_d) return fail(E_INVALID, "moe-gemv: null argument");
+    const int tw = src0->type;
+    if (!type_supported(tw)) return fail(E_UNSUPPORTED, "moe-gemv: unsupported expert type %d", tw);
+    const TypeGeom g = type_geom(tw);
+    if (ne00 <= 0 || ne01 <= 0 || ne02 <= 0 || ncols_dst <= 0 || nchannels_dst <= 0 || nchannels_y <= 0)
+        return fail(E_INVALID, "moe-gemv: empty shape");
+    if (ne00 % g.unit_elems) return fail(E_UNSUPPORTED, "moe-gemv: ne00=%lld is not a multiple of %d", (long long) ne00, g.unit_elems);
+    if (ne00 / g.unit_elems > WAVE) return fail(E_UNSUPPORTED, "moe-gemv: ne00=%lld exceeds %d units per row", (long long) ne00, WAVE);
+    if (src0->ne[0] != ne00 || src0->ne[1] != ne01 || src0->ne[2] != ne02 || !is_contiguous(src0))
+        return fail(E_INVALID, "moe-gemv: src0 shape/strides do not match the call");
+    if (act != ACT_Q8_1 && act != ACT_Q8_K) return fail(E_INVALID, "moe-gemv: unknown activation format %d", act);
+    if (act == ACT_Q8_K && !g.kquant) return fail(E_UNSUPPORTED, "moe-gemv: q8_K activations need K-quant weights");
+    const size_t eb = (size_t) src0->nb[2];
+    if (eb > 0xFFFFFFF0ull) return fail(E_UNSUPPORTED, "moe-gemv: expert matrix larger than 4 GiB");
+    if (ids_stride < nchannels_dst) return fail(E_INVALID, "moe-gemv: ids_stride < nchannels_dst");
+    if (ne02 > 4096) return fail(E_UNSUPPORTED, "moe-gemv: more than 4096 experts cannot be packed in the miss log");
+
+    int ts = 0;
+    const void *sh_up = fusion ? fusion->shared_up : nullptr;
+    if (sh_up) {
+        ts = fusion->shared_type < 0 ? tw : fusion->shared_type;
+        if (!type_supported(ts)) return fail(E_UNSUPPORTED, "moe-gemv: unsupported shared-expert type %d", ts);
+        if (ne00 % type_geom(ts).unit_elems || ne00 / type_geom(ts).unit_elems > WAVE)
+            return fail(E_UNSUPPORTED, "moe-gemv: shared-expert row length not supported");
+        if (act == ACT_Q8_K && !type_geom(ts).kquant) return fail(E_UNSUPPORTED, "moe-gemv: q8_K activations need a K-quant shared expert");
+        if (!fusion->shared_dst) return fail(E_INVALID, "moe-gemv: shared_up without shared_dst");
+    }
+    const bool aligned_ok = g.aligned ? ((((uintptr_t) src0->data) | eb) & 3u) == 0 : ((((uintptr_t) src0->data) | eb) & 1u) == 0;
+    if (!aligned_ok) return fail(E_UNSUPPORTED, "moe-gemv: expert base/size alignment not supported");
+
+    GemvArgs a = {};
+    const int ablk_bytes = act == ACT_Q8_1 ? 36 : 292;
+    const int ablk_elems = act == ACT_Q8_1 ? 32 : 256;
+    if (ne00 % ablk_elems) return fail(E_INVALID, "moe-gemv: ne00 not a multiple of the activation block");
+    const int64_t act_row = ne00 / ablk_elems * ablk_bytes;
+    a.y = (const uint8_t *) src1;
+    a.stride_col_y = stride_col_y * ablk_bytes;
+    a.stride_channel_y = stride_channel_y * ablk_bytes;
+    a.nchannels_y = (uint32_t) nchannels_y;
+    const int64_t y_extent = (nchannels_y - 1) * a.stride_channel_y + (ncols_dst - 1) * a.stride_col_y + act_row;
+    if (y_extent <= 0 || y_extent > 0xFFFFFFF0ll) return fail(E_INVALID, "moe-gemv: activation extent out of range");
+    a.y_bytes = (uint64_t) y_extent;
+    a.ids = ids_d;
+    a.ids_stride = ids_stride;
+    a.dst = dst_d;
+    a.stride_col_dst = stride_col_dst;
+    a.stride_channel_dst = stride_channel_dst;
+    a.ncols = (int32_t) ne00;
+    a.nrows = (int32_t) ne01;
+    a.n_used = (int32_t) nchannels_dst;
+    a.n_tok = (int32_t) ncols_dst;
+    a.n_experts = (int32_t) ne02;
+    a.expert_bytes = eb;
+    a.cache_id = -1;
+    a.cache_id_gate = -1;
+    a.glu_op = 2;                  // SWIGLU unless the fusion says otherwise (kernels/moe-cache.cu:116)
+    a.bias_stride = stride_channel_dst;
+    if (fusion) {
+        a.x_bias = fusion->x_bias;
+        a.gate_bias = fusion->gate_bias;
+        a.x_scale = fusion->x_scale;
+        a.gate_scale = fusion->gate_scale;
+        a.bias_stride = fusion->bias_stride > 0 ? fusion->bias_stride : stride_channel_dst;
+        a.glu_op = fusion->glu_op;
+        a.glu_limit = fusion->glu_limit;
+        if (sh_up) {
+            a.sh_up = (const uint8_t *) sh_up;
+            a.sh_gate = (const uint8_t *) fusion->shared_gate;
+            a.sh_dst = fusion->shared_dst;
+            a.sh_stride_col_dst = fusion->shared_stride_col_dst;
+            a.sh_matrix_bytes = (uint64_t) (ne00 / type_geom(ts).block_elems) * type_geom(ts).block_bytes * (uint64_t) ne01;
+            if (fusion->shared_src1) {
+                a.sh_y = (const uint8_t *) fusion->shared_src1;
+                a.sh_stride_col_y = fusion->shared_stride_col_y * ablk_bytes;
+                a.sh_y_bytes = (uint64_t) ((ncols_dst - 1) * a.sh_stride_col_y + act_row);
+            }
+        }
+    }
+
+    const bool gate_wants = use_cache && gate_host ? wants_impl(gate_host) : false;
+    std::lock_guard<std::mutex> lock(g_mutex);
+    read_env_locked();
+    int rc;
+    if (use_cache) {
+        if (!g_cfg.enabled) return fail(E_DISABLED, "moe-cache: not enabled (GGML_HIP_MOE_CACHE)");
+        Entry *e = nullptr, *ge = nullptr;
+        if ((rc = get_or_create_locked(src0, stream, &e))) return rc;
+        a.tbl = e->d_tbl;
+        a.stamps = e->d_stamps;
+        a.cache_id = e->id;
+        a.stats = g_d_stats;
+        a.clock = g_d_clock;
+        if (gate_host && fusion && fusion->gate) {
+            return fail(E_INVALID, "moe-gemv: gate given both as host tensor and as device pointer");
+        }
+        if (gate_host) {
+            if (gate_host->type != tw || gate_host->ne[0] != ne00 || gate_host->ne[1] != ne01 || gate_host->ne[2] != ne02 ||
+                gate_host->nb[2] != src0->nb[2])
+                return fail(E_INVALID, "moe-gemv: gate tensor does not match src0");
+            if (gate_wants) {
+                if ((rc = get_or_create_locked(gate_host, stream, &ge))) return rc;
+                a.tbl_gate = ge->d_tbl;
+                a.stamps_gate = ge->d_stamps;
+                a.cache_id_gate = ge->id;
+            } else {
+                Resident *r;
+                if ((rc = resident_table_locked(gate_host->data, (int) ne02, eb, stream, &r))) return rc;
+                a.tbl_gate = r->d_tbl;
+            }
+            a.has_gate = 1;
+        }
+    } else {
+        Resident *r;
+        if ((rc = resident_table_locked(src0->data, (int) ne02, eb, stream, &r))) return rc;
+        a.tbl = r->d_tbl;
+    }
+    if (fusion && fusion->gate) {
+        Resident *r;
+        if ((rc = resident_table_locked(fusion->gate, (int) ne02, eb, stream, &r))) return rc;
+        a.tbl_gate = r->d_tbl;
+        a.has_gate = 1;
+    }
+    if ((rc = dev()->launch_gemv(a, tw, ts, act, stream))) return dev_err(rc, "GEMV launch");
+    return 0;
+}
+
+int quantize_common(int kind, const float *x, void *y, int64_t k, int64_t nrows, int64_t x_stride, int64_t y_stride, void *stream) {
+    const int be = kind == 1 ? 256 : 32;
+    const int bb = kind == 1 ? 292 : 36;
+    if (!x || !y) return fail(E_INVALID, "quantize: null argument");
+    if (k <= 0 || nrows < 0 || k % be) return fail(E_INVALID, "quantize: k=%lld must be a positive multiple of %d", (long long) k, be);
+    if (x_stride < k || y_stride < k / be) return fail(E_INVALID, "quantize: row stride smaller than the row");
+    if (((uintptr_t) y & 3u) || ((uintptr_t) x & 3u)) return fail(E_INVALID, "quantize: misaligned buffers");
+    QuantArgs q;
+    q.x = x;
+    q.y = (uint8_t *) y;
+    q.k = k;
+    q.nrows = nrows;
+    q.x_stride = x_stride;
+    q.y_stride = y_stride * bb;
+    const int rc = dev()->launch_quantize(kind, q, stream);
+    if (rc) return dev_err(rc, "quantize launch");
+    return 0;
+}
+
+}  // namespace
+}  // namespace mc
+
+using namespace mc;
+
+extern "C" {
+
+int ggml_hip_moe_cache_enabled(void) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    read_env_locked();
+    return g_cfg.enabled ? 1 : 0;
+}
+
+int ggml_hip_moe_cache_wants(const ggml_hip_moe_tensor *src0) { return wants_impl(src0) ? 1 : 0; }
+
+int ggml_hip_moe_cache_mul_mat_vec_q(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *gate_host,
+                                     const ggml_hip_moe_fusion *fusion, const void *src1_q8_1, const int32_t *ids_d,
+                                     float *dst_d, int64_t ne00, int64_t ne01, int64_t ne02, int64_t ne03,
+                                     int64_t ncols_dst, int64_t s01, int64_t s02, int64_t s03, int64_t nchannels_y,
+                                     int64_t nchannels_dst, int64_t stride_col_y, int64_t stride_col_dst,
+                                     int64_t stride_channel_y, int64_t stride_channel_dst, int64_t ids_stride, void *stream) {
+    (void) s02; (void) s03;
+    if (!src0) return fail(E_INVALID, "moe-gemv: null src0");
+    if (ne03 != 1) return fail(E_UNSUPPORTED, "moe-gemv: ne03 != 1");
+    const TypeGeom g = type_geom(src0->type);
+    if (g.block_elems && s01 != ne00 / g.block_elems) return fail(E_UNSUPPORTED, "moe-gemv: non-contiguous rows (s01)");
+    if (!wants_impl(src0)) return fail(E_STATE, "moe-cache: src0 does not qualify for the cache path (wants() == 0)");
+    return gemv_common(1, ACT_Q8_1, src0, gate_host, fusion, src1_q8_1, ids_d, dst_d, ne00, ne01, ne02, ncols_dst, nchannels_y,
+                       nchannels_dst, stride_col_y, stride_col_dst, stride_channel_y, stride_channel_dst, ids_stride, stream);
+}
+
+int ggml_hip_mul_mat_vec_q_moe(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_fusion *fusion, const void *src1_q8_1,
+                               const int32_t *ids_d, float *dst_d, int64_t ne00, int64_t ne01, int64_t ne02, int64_t ne03,
+                               int64_t ncols_dst, int64_t s01, int64_t s02, int64_t s03, int64_t nchannels_y,
+                               int64_t nchannels_dst, int64_t stride_col_y, int64_t stride_col_dst, int64_t stride_channel_y,
+                               int64_t stride_channel_dst, int64_t ids_stride, void *stream) {
+    (void) s02; (void) s03;
+    if (!src0) return fail(E_INVALID, "moe-gemv: null src0");
+    if (ne03 != 1) return fail(E_UNSUPPORTED, "moe-gemv: ne03 != 1");
+    const TypeGeom g = type_geom(src0->type);
+    if (g.block_elems && s01 != ne00 / g.block_elems) return fail(E_UNSUPPORTED, "moe-gemv: non-contiguous rows (s01)");
+    return gemv_common(0, ACT_Q8_1, src0, nullptr, fusion, src1_q8_1, ids_d, dst_d, ne00, ne01, ne02, ncols_dst, nchannels_y,
+                       nchannels_dst, stride_col_y, stride_col_dst, stride_channel_y, stride_channel_dst, ids_stride, stream);
+}
+
+int ggml_hip_moe_mul_mat_vec_ex(int use_cache, int act_format, const ggml_hip_moe_tensor *src0,
+                                const ggml_hip_moe_tensor *gate_host, const ggml_hip_moe_fusion *fusion, const void *src1,
+                                const int32_t *ids_d, float *dst_d, int64_t ne00, int64_t ne01, int64_t ne02,
+                                int64_t ncols_dst, int64_t nchannels_y, int64_t nchannels_dst, int64_t stride_col_y,
+                                int64_t stride_col_dst, int64_t stride_channel_y, int64_t stride_channel_dst,
+                                int64_t ids_stride, void *stream) {
+    if (use_cache && !wants_impl(src0)) return fail(E_STATE, "moe-cache: src0 does not qualify for the cache path (wants() == 0)");
+    if (!use_cache && gate_host) return fail(E_INVALID, "moe-gemv: gate_host is for the cache path; pass fusion->gate");
+    return gemv_common(use_cache ? 1 : 0, act_format, src0, gate_host, fusion, src1, ids_d, dst_d, ne00, ne01, ne02, ncols_dst,
+                       nchannels_y, nchannels_dst, stride_col_y, stride_col_dst, stride_channel_y, stride_channel_dst,
+                       ids_stride, stream);
+}
+
+int ggml_hip_moe_cache_step(void *stream) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    read_env_locked();
+    if (!g_cfg.enabled || g_all.empty()) return 0;
+    return step_locked(stream);
+}
+
+int ggml_hip_moe_cache_active(void) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    return g_all.empty() ? 0 : 1;
+}
+
+int ggml_hip_moe_cache_pin_host(const ggml_hip_moe_tensor *t) {
+    {
+        std::lock_guard<std::mutex> lock(g_mutex);
+        read_env_locked();
+        if (!g_cfg.enabled) return 0;
+    }
+    if (!t || !t->has_buffer || !t->data) return 0;
+    const int kind = dev()->ptr_kind(t->data);
+    if (kind == PTR_HOST) return 1;
+    if (kind == PTR_DEVICE || kind == PTR_ERROR) return 0;
+    if (!g_cfg.allow_register) {
+        fail(E_STATE, "moe-cache: %s is not GPU-readable; allocate it with hipHostMalloc or set GGML_HIP_MOE_CACHE_ALLOW_REGISTER=1",
+             t->name ? t->name : "<tensor>");
+        return 0;
+    }
+    const uintptr_t page = 4096;
+    const uintptr_t base = (uintptr_t) t->data & ~(page - 1);
+    const uint64_t nbytes = t->nb[3] ? t->nb[3] : t->nb[2] * (uint64_t) t->ne[2];
+    const uintptr_t end = ((uintptr_t) t->data + nbytes + page - 1) & ~(page - 1);
+    const int rc = dev()->register_host((void *) base, end - base);
+    {
+        std::lock_guard<std::mutex> lock(g_ptr_mutex);
+        g_ptr_kind.erase(t->data);
+    }
+    if (rc) {
+        fail(E_DEVICE, "moe-cache: failed to pin %s: %s", t->name ? t->name : "<tensor>", dev()->error_string(rc));
+        return 0;
+    }
+    return 1;
+}
+
+int ggml_hip_quantize_q8_1(const float *x, void *y, int64_t k, int64_t nrows, int64_t x_stride, int64_t y_stride, void *stream) {
+    return quantize_common(0, x, y, k, nrows, x_stride, y_stride, stream);
+}
+
+int ggml_hip_quantize_q8_K(const float *x, void *y, int64_t k, int64_t nrows, int64_t x_stride, int64_t y_stride, void *stream) {
+    return quantize_common(1, x, y, k, nrows, x_stride, y_stride, stream);
+}
+
+int ggml_hip_quantize_q8_0_as_q8_1(const float *x, void *y, int64_t k, int64_t nrows, int64_t x_stride, int64_t y_stride,
+                                   void *stream) {
+    return quantize_common(2, x, y, k, nrows, x_stride, y_stride, stream);
+}
+
+int ggml_hip_moe_cache_configure(const ggml_hip_moe_config *cfg) {
+    if (!cfg) return fail(E_INVALID, "configure: null config");
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (!g_all.empty()) return fail(E_STATE, "configure: tensors are already registered (call reset first)");
+    Config c;
+    c.enabled = cfg->enabled != 0;
+    c.slots = cfg->slots;
+    c.budget_gb = cfg->budget_gb;
+    c.margin_gb = cfg->margin_gb >= 0 ? cfg->margin_gb : 2.0;
+    c.seed_path = cfg->seed_path ? cfg->seed_path : "";
+    c.max_promotions = cfg->max_promotions >= 0 ? cfg->max_promotions : DEFAULT_MAX_PROMOTIONS;
+    c.verbose = cfg->verbose != 0;
+    c.debug = false;
+    c.allow_register = g_cfg.allow_register;
+    g_cfg = c;
+    g_cfg_ready = true;
+    g_seed.clear();
+    g_seed_loaded = false;
+    return 0;
+}
+
+int ggml_hip_moe_cache_get_config(ggml_hip_moe_config *out) {
+    if (!out) return fail(E_INVALID, "get_config: null");
+    std::lock_guard<std::mutex> lock(g_mutex);
+    read_env_locked();
+    out->enabled = g_cfg.enabled;
+    out->slots = g_cfg.slots;
+    out->budget_gb = g_cfg.budget_gb;
+    out->margin_gb = g_cfg.margin_gb;
+    out->seed_path = g_cfg.seed_path.c_str();
+    out->max_promotions = g_cfg.max_promotions;
+    out->verbose = g_cfg.verbose;
+    return 0;
+}
+
+int ggml_hip_moe_cache_num_entries(void) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    return (int) g_all.size();
+}
+
+int ggml_hip_moe_cache_entry_info(int32_t id, ggml_hip_moe_entry_info *out) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (!out || id < 0 || id >= (int32_t) g_all.size()) return fail(E_INVALID, "entry_info: bad id %d", id);
+    const Entry *e = g_all[id];
+    out->id = e->id;
+    out->type = e->type;
+    out->n_experts = e->n_experts;
+    out->n_slots = e->n_slots;
+    out->expert_bytes = e->expert_bytes;
+    int res = 0;
+    for (int s = 0; s < e->n_slots; ++s) res += e->expert_of[s] >= 0;
+    out->n_resident = res;
+    out->stamps_clock = e->stamps_clock;
+    return 0;
+}
+
+int ggml_hip_moe_cache_entry_slots(int32_t id, int32_t *slot_of, int32_t n_experts, int32_t *expert_of, int32_t n_slots) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (id < 0 || id >= (int32_t) g_all.size()) return fail(E_INVALID, "entry_slots: bad id %d", id);
+    const Entry *e = g_all[id];
+    if (slot_of) {
+        if (n_experts < e->n_experts) return fail(E_INVALID, "entry_slots: slot_of too small");
+        memcpy(slot_of, e->slot_of.data(), sizeof(int32_t) * e->n_experts);
+    }
+    if (expert_of) {
+        if (n_slots < e->n_slots) return fail(E_INVALID, "entry_slots: expert_of too small");
+        if (e->n_slots) memcpy(expert_of, e->expert_of.data(), sizeof(int32_t) * e->n_slots);
+    }
+    return 0;
+}
+
+int ggml_hip_moe_cache_entry_table(int32_t id, int32_t *out, int32_t n_experts) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (id < 0 || id >= (int32_t) g_all.size()) return fail(E_INVALID, "entry_table: bad id %d", id);
+    const Entry *e = g_all[id];
+    if (!out || n_experts < e->n_experts) return fail(E_INVALID, "entry_table: buffer too small");
+    for (int i = 0; i < e->n_experts; ++i) {
+        const uint64_t v = e->h_tbl[i];
+        if (v & 1ull) {
+            if (v != host_entry(e, i)) return fail(E_STATE, "entry_table: corrupt host entry %d", i);
+            out[i] = -1;
+        } else {
+            const uint64_t off = v - (uint64_t) (uintptr_t) e->pool;
+            if (!e->pool || off % e->expert_bytes || off / e->expert_bytes >= (uint64_t) e->n_slots)
+                return fail(E_STATE, "entry_table: corrupt pool entry %d", i);
+            out[i] = (int32_t) (off / e->expert_bytes);
+        }
+    }
+    return 0;
+}
+
+int ggml_hip_moe_cache_entry_device(int32_t id, void **d_tbl, void **d_stamps, void **pool) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (id < 0 || id >= (int32_t) g_all.size()) return fail(E_INVALID, "entry_device: bad id %d", id);
+    const Entry *e = g_all[id];
+    if (d_tbl) *d_tbl = e->d_tbl;
+    if (d_stamps) *d_stamps = e->d_stamps;
+    if (pool) *pool = e->pool;
+    return 0;
+}
+
+int ggml_hip_moe_cache_device_globals(void **d_stats, void **d_clock) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (d_stats) *d_stats = g_d_stats;
+    if (d_clock) *d_clock = g_d_clock;
+    return 0;
+}
+
+int ggml_hip_moe_cache_stats_snapshot(uint32_t *out, int32_t n_words, void *stream) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (!out || n_words < 0 || n_words > STATS_WORDS) return fail(E_INVALID, "stats_snapshot: bad buffer");
+    if (!g_d_stats) return fail(E_STATE, "stats_snapshot: nothing registered");
+    int rc;
+    if ((rc = dev()->copy_d2h(out, g_d_stats, sizeof(uint32_t) * n_words, stream))) return dev_err(rc, "stats snapshot");
+    if ((rc = dev()->sync(stream))) return dev_err(rc, "stream sync");
+    return 0;
+}
+
+int ggml_hip_moe_cache_stamps_snapshot(int32_t id, uint32_t *out, int32_t n, void *stream) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (id < 0 || id >= (int32_t) g_all.size()) return fail(E_INVALID, "stamps_snapshot: bad id %d", id);
+    const Entry *e = g_all[id];
+    if (!out || n < e->n_experts) return fail(E_INVALID, "stamps_snapshot: buffer too small");
+    int rc;
+    if ((rc = dev()->copy_d2h(out, e->d_stamps, sizeof(uint32_t) * e->n_experts, stream))) return dev_err(rc, "stamps snapshot");
+    if ((rc = dev()->sync(stream))) return dev_err(rc, "stream sync");
+    return 0;
+}
+
+int ggml_hip_moe_cache_totals(ggml_hip_moe_totals *out) {
+    if (!out) return fail(E_INVALID, "totals: null");
+    std::lock_guard<std::mutex> lock(g_mutex);
+    *out = g_totals;
+    out->clock = g_h_clock;
+    out->admission_size = (uint32_t) g_admission.size();
+    return 0;
+}
+
+int ggml_hip_moe_cache_reset(void) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    int first_rc = 0;
+    auto note = [&](int rc) { if (rc && !first_rc) first_rc = rc; };
+    for (Entry *e : g_all) {
+        if (e->pool) note(dev()->free_dev(e->pool));
+        if (e->d_tbl) note(dev()->free_dev(e->d_tbl));
+        if (e->d_stamps) note(dev()->free_dev(e->d_stamps));
+        delete e;
+    }
+    g_all.clear();
+    g_by_data.clear();
+    for (auto &kv : g_resident) {
+        if (kv.second->d_tbl) note(dev()->free_dev(kv.second->d_tbl));
+        delete kv.second;
+    }
+    g_resident.clear();
+    if (g_d_stats) note(dev()->free_dev(g_d_stats));
+    if (g_d_clock) note(dev()->free_dev(g_d_clock));
+    if (g_h_stats) note(dev()->free_host(g_h_stats));
+    g_d_stats = g_d_clock = g_h_stats = nullptr;
+    g_h_clock = 0;
+    g_used = 0;
+    g_admission.clear();
+    g_seed.clear();
+    g_seed_loaded = false;
+    g_totals = {};
+    {
+        std::lock_guard<std::mutex> l2(g_ptr_mutex);
+        g_ptr_kind.clear();
+    }
+    if (first_rc) return dev_err(first_rc, "reset free");
+    return 0;
+}
+
+const char *ggml_hip_moe_last_error(void) { return t_last_error.c_str(); }
+
+const char *ggml_hip_moe_version(void) { return "ggml-hip-moe-cache 0.1 (gfx950)"; }
+
+}  // extern "C"

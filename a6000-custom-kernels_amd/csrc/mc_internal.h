@@ -1,0 +1,130 @@
+// mc_internal.h -- shared between the C++ host code and the gfx950 kernels.
+//
+// Geometry of the GEMV: each 64-lane wavefront owns one "step" of a routed
+// pick (or of the shared expert): rows_per_step consecutive rows of one expert
+// matrix.  A row is split into `nu` lane units of UNIT_ELEMS values; one lane
+// computes one unit.  K-quant units are one 256-value super-block; legacy
+// units are two 32-value blocks (so every unit starts on a 4-byte boundary).
+#ifndef MC_INTERNAL_H
+#define MC_INTERNAL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace mc {
+
+enum : int {
+    T_F32 = 0, T_Q4_0 = 2, T_Q5_0 = 6, T_Q8_0 = 8, T_Q8_1 = 9,
+    T_Q2_K = 10, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_Q8_K = 15
+};
+
+enum : int { ACT_Q8_1 = 0, ACT_Q8_K = 1 };
+
+// Device stats buffer: [0] miss count, [1] resident-hit count,
+// [2 .. 2+MISS_CAP) miss log of (cache_id << 12 | expert) entries
+// (kernels/moe-cache.cu:34-40).
+constexpr int MISS_CAP = 8190;
+constexpr int HIT_WORD = 1;
+constexpr int LOG_BASE = 2;
+constexpr int STATS_WORDS = 2 + MISS_CAP;
+constexpr int DEFAULT_MAX_PROMOTIONS = 48;
+
+constexpr int WAVE = 64;
+
+struct TypeGeom {
+    int block_elems;
+    int block_bytes;
+    int unit_elems;   // values per lane unit
+    int unit_bytes;   // bytes per lane unit
+    int aligned;      // 1: unit offsets are multiples of 4 bytes; 0: only of 2
+    int kquant;
+};
+
+inline constexpr TypeGeom type_geom(int t) {
+    return t == T_Q4_0 ? TypeGeom{32, 18, 64, 36, 1, 0}
+         : t == T_Q5_0 ? TypeGeom{32, 22, 64, 44, 1, 0}
+         : t == T_Q8_0 ? TypeGeom{32, 34, 64, 68, 1, 0}
+         : t == T_Q2_K ? TypeGeom{256, 84, 256, 84, 1, 1}
+         : t == T_Q3_K ? TypeGeom{256, 110, 256, 110, 0, 1}
+         : t == T_Q4_K ? TypeGeom{256, 144, 256, 144, 1, 1}
+         : t == T_Q5_K ? TypeGeom{256, 176, 256, 176, 1, 1}
+         : t == T_Q6_K ? TypeGeom{256, 210, 256, 210, 0, 1}
+         : TypeGeom{0, 0, 0, 0, 0, 0};
+}
+
+inline constexpr bool type_supported(int t) { return type_geom(t).block_elems != 0; }
+
+// Bytes of LDS one wave needs to stage one step of one matrix: the step's
+// byte span (<= 64 units) plus up to 15 bytes of lead-in to the 16-byte
+// aligned start and 4 bytes of over-read, in whole 1 KiB DMA rounds.
+inline constexpr int span_lds_bytes(int t) {
+    return ((WAVE * type_geom(t).unit_bytes + 20 + 1023) / 1024) * 1024;
+}
+
+// Kernel arguments (passed by value).
+struct GemvArgs {
+    // routed experts, resolved through tagged pointer tables (LSB=1: host memory)
+    const uint64_t *tbl;          // [n_experts] up / plain projection
+    const uint64_t *tbl_gate;     // [n_experts] gate projection, or null
+    uint32_t *stamps;             // [n_experts] last-use clock of tbl's tensor, or null
+    uint32_t *stamps_gate;        // [n_experts] of tbl_gate's tensor, or null
+    uint32_t *stats;              // [STATS_WORDS], or null (no recording)
+    const uint32_t *clock;        // device LRU clock (read, never a kernel-argument value)
+    int32_t cache_id;             // registry id of tbl's tensor
+    int32_t cache_id_gate;        // registry id of tbl_gate's tensor (-1: none)
+    int32_t n_experts;
+    int32_t has_gate;             // 1: fused gate present (through tbl_gate)
+    uint64_t expert_bytes;        // bytes of one expert matrix
+    // activations
+    const uint8_t *y;             // activation base (q8_1 or q8_K blocks)
+    uint64_t y_bytes;             // addressable bytes from y (buffer range)
+    int64_t stride_col_y;         // bytes between tokens
+    int64_t stride_channel_y;     // bytes between channels
+    uint32_t nchannels_y;
+    const int32_t *ids;           // [n_tok][ids_stride]
+    int64_t ids_stride;           // int32 elements
+    // outputs
+    float *dst;
+    int64_t stride_col_dst;       // floats between tokens
+    int64_t stride_channel_dst;   // floats between channels (picks)
+    // fusion
+    const float *x_bias;
+    const float *gate_bias;
+    const float *x_scale;
+    const float *gate_scale;
+    int64_t bias_stride;          // floats per expert
+    int32_t glu_op;
+    float glu_limit;
+    // shared expert (dense)
+    const uint8_t *sh_up;
+    const uint8_t *sh_gate;
+    float *sh_dst;
+    int64_t sh_stride_col_dst;
+    const uint8_t *sh_y;          // null: channel 0 of y
+    uint64_t sh_y_bytes;
+    int64_t sh_stride_col_y;      // bytes between tokens of sh_y
+    uint64_t sh_matrix_bytes;     // bytes of the shared matrix
+    // shape
+    int32_t ncols;                // K (ne00)
+    int32_t nrows;                // rows per expert (ne01)
+    int32_t n_used;               // picks per token (nchannels_dst)
+    int32_t n_tok;                // tokens (ncols_dst)
+    // tiling (filled by the launcher)
+    int32_t tiles_per_pick;
+    int32_t sh_tiles_per_tok;
+    int32_t n_routed_tiles;
+    int32_t n_tiles;
+};
+
+struct QuantArgs {
+    const float *x;
+    uint8_t *y;
+    int64_t k;          // values per row
+    int64_t nrows;
+    int64_t x_stride;   // floats between rows
+    int64_t y_stride;   // bytes between rows
+};
+
+}  // namespace mc
+
+#endif

@@ -1,0 +1,267 @@
+/*
+ * ggml_hip_moe_cache.h -- C ABI of the MI355X (gfx950) pointer-table quantized
+ * MoE expert GEMV and its hot-expert HBM cache.
+ *
+ * Drop-in boundary for ggml's HIP backend.  Every entry point below replaces
+ * one function of the reference's kernels/moe-cache.cuh (cited per function).
+ * The ABI is plain C: tensors are described by POD mirrors of the ggml fields
+ * the path consumes, streams are passed as `void *` holding a hipStream_t, and
+ * every function returns a status instead of aborting (the reference aborts
+ * through CUDA_CHECK / GGML_ABORT: kernels/moe-cache.cu:475-480, 864).
+ *
+ * Status codes: 0 = success, < 0 = error (text in ggml_hip_moe_last_error()).
+ * Boolean predicates return 1 / 0.
+ *
+ * Ownership (kernels/moe-cache.cu:568-581): the library owns the pool, the
+ * pointer tables, the stamp arrays and the global stats/clock it allocates;
+ * the caller owns weights, host expert memory, activations, ids and outputs.
+ * Host expert memory must outlive the library's use of it.
+ *
+ * Threading: registry and step work is serialized by one mutex
+ * (kernels/moe-cache.cu:321, 526, 674); ggml_hip_moe_cache_wants() may be
+ * called concurrently (kernels/moe-cache.cu:425-440).  All device work of one
+ * call is ordered on the caller's stream.  Kernel arguments never change
+ * between steps (the LRU clock is read from device memory), so a captured
+ * hipGraph stays valid; ggml_hip_moe_cache_step() must run outside capture.
+ */
+#ifndef GGML_HIP_MOE_CACHE_H
+#define GGML_HIP_MOE_CACHE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml_type values used by the path (ggml.h numbering) */
+enum {
+    GGML_HIP_MOE_TYPE_F32  = 0,
+    GGML_HIP_MOE_TYPE_Q4_0 = 2,
+    GGML_HIP_MOE_TYPE_Q5_0 = 6,
+    GGML_HIP_MOE_TYPE_Q8_0 = 8,
+    GGML_HIP_MOE_TYPE_Q8_1 = 9,
+    GGML_HIP_MOE_TYPE_Q2_K = 10,
+    GGML_HIP_MOE_TYPE_Q3_K = 11,
+    GGML_HIP_MOE_TYPE_Q4_K = 12,
+    GGML_HIP_MOE_TYPE_Q5_K = 13,
+    GGML_HIP_MOE_TYPE_Q6_K = 14,
+    GGML_HIP_MOE_TYPE_Q8_K = 15
+};
+
+/* ggml_glu_op values, plus the clamped SwiGLU the reference's epilogue names
+ * (kernels/moe-cache.cu:264-280). */
+enum {
+    GGML_HIP_MOE_GLU_REGLU        = 0,
+    GGML_HIP_MOE_GLU_GEGLU        = 1,
+    GGML_HIP_MOE_GLU_SWIGLU       = 2,
+    GGML_HIP_MOE_GLU_SWIGLU_OAI   = 3,
+    GGML_HIP_MOE_GLU_GEGLU_ERF    = 4,
+    GGML_HIP_MOE_GLU_GEGLU_QUICK  = 5,
+    GGML_HIP_MOE_GLU_SWIGLU_CLAMP = 6
+};
+
+/* Activation formats accepted by the GEMV (src1 after quantization). */
+enum {
+    GGML_HIP_MOE_ACT_Q8_1 = 0, /* ggml-CUDA q8_1 blocks (36 B / 32 values): the reference's src1_q8_1 */
+    GGML_HIP_MOE_ACT_Q8_K = 1  /* ggml-CPU q8_K blocks (292 B / 256 values), K-quant weights only */
+};
+
+/* POD mirror of the ggml_tensor fields the path reads
+ * (kernels/moe-cache.cu:87, 442-469, 525-541): type, ne, nb, data, name,
+ * buffer (!= NULL) and view_src (!= NULL). */
+typedef struct ggml_hip_moe_tensor {
+    int32_t     type;
+    int64_t     ne[4];
+    uint64_t    nb[4];
+    void       *data;
+    const char *name;
+    int32_t     has_buffer;
+    int32_t     is_view;
+} ggml_hip_moe_tensor;
+
+/* Mirror of ggml_cuda_mm_fusion_args_device as the reference reads it
+ * (kernels/moe-cache.cu:103-129), plus explicit fields for what the reference
+ * leaves implicit. */
+typedef struct ggml_hip_moe_fusion {
+    const void  *gate;              /* device gate expert tensor (same type/shape as src0) when it has no table */
+    const float *x_bias;            /* [n_experts][bias_stride] added to the up/plain output */
+    const float *gate_bias;         /* [n_experts][bias_stride] added to the gate output */
+    const float *x_scale;           /* [n_experts] multiplies the up/plain output (before bias) */
+    const float *gate_scale;        /* [n_experts] multiplies the gate output (before bias) */
+    int32_t      glu_op;            /* GGML_HIP_MOE_GLU_*; used when a gate is present (SWIGLU when fusion is NULL) */
+    float        glu_limit;         /* SWIGLU_CLAMP limit */
+    const void  *shared_up;         /* dense shared expert [ne01 x ne00], device memory */
+    const void  *shared_gate;       /* dense shared gate, device memory, or NULL */
+    float       *shared_dst;        /* shared expert output; token t at shared_dst + t*shared_stride_col_dst */
+    int64_t      shared_stride_col_dst;
+    /* -- extensions -- */
+    int32_t      shared_type;       /* ggml_type of shared_up/shared_gate; < 0: same as src0 */
+    const void  *shared_src1;       /* activation rows of the shared expert; NULL: channel 0 of src1 */
+    int64_t      shared_stride_col_y; /* activation blocks between tokens of shared_src1 */
+    int64_t      bias_stride;       /* floats per expert in x_bias/gate_bias; 0: stride_channel_dst */
+} ggml_hip_moe_fusion;
+
+/* ---------------------------------------------------------------------
+ * Reference API (kernels/moe-cache.cuh:15-40)
+ * --------------------------------------------------------------------- */
+
+/* replaces ggml_cuda_moe_cache_enabled (kernels/moe-cache.cuh:15, moe-cache.cu:345-363):
+ * GGML_HIP_MOE_CACHE (or GGML_CUDA_MOE_CACHE) set and not "0". */
+int ggml_hip_moe_cache_enabled(void);
+
+/* replaces ggml_cuda_moe_cache_wants (kernels/moe-cache.cuh:18, moe-cache.cu:442-469):
+ * enabled, host-resident GPU-readable memory, supported type, ne[2] >= 2,
+ * ne[3] == 1, not a view, contiguous. */
+int ggml_hip_moe_cache_wants(const ggml_hip_moe_tensor *src0);
+
+/* replaces ggml_cuda_moe_cache_mul_mat_vec_q (kernels/moe-cache.cuh:21-31, moe-cache.cu:821-868).
+ * Registers src0 (and a host-resident gate) on first use, then runs the
+ * pointer-table GEMV on `stream`.  Argument meaning follows the reference:
+ * s01 is the weight row stride in blocks, stride_col_y / stride_channel_y are
+ * in activation blocks (q8_1: 32 values), stride_col_dst / stride_channel_dst
+ * in floats, ids_stride in int32 elements.  gate_host is the host-side fused
+ * gate tensor (ggml_cuda_mm_fusion_args_host::gate) or NULL; fusion may be NULL. */
+int ggml_hip_moe_cache_mul_mat_vec_q(
+        const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *gate_host,
+        const ggml_hip_moe_fusion *fusion,
+        const void *src1_q8_1, const int32_t *ids_d, float *dst_d,
+        int64_t ne00, int64_t ne01, int64_t ne02, int64_t ne03,
+        int64_t ncols_dst, int64_t s01, int64_t s02, int64_t s03,
+        int64_t nchannels_y, int64_t nchannels_dst,
+        int64_t stride_col_y, int64_t stride_col_dst,
+        int64_t stride_channel_y, int64_t stride_channel_dst,
+        int64_t ids_stride, void *stream);
+
+/* replaces ggml_cuda_moe_cache_step (kernels/moe-cache.cuh:34, moe-cache.cu:669-775):
+ * miss-log readback, clock advance, 2nd-sighting admission, LRU eviction,
+ * pool copies and batched table flush.  Call between graph launches. */
+int ggml_hip_moe_cache_step(void *stream);
+
+/* replaces ggml_cuda_moe_cache_active (kernels/moe-cache.cuh:37, moe-cache.cu:365-368) */
+int ggml_hip_moe_cache_active(void);
+
+/* replaces ggml_cuda_moe_cache_pin_host (kernels/moe-cache.cuh:40, moe-cache.cu:372-405):
+ * 1 when t->data is (now) GPU-readable host memory.  Memory that is not yet
+ * registered is registered only when GGML_HIP_MOE_CACHE_ALLOW_REGISTER=1;
+ * memory from hipHostMalloc is recognized without registration. */
+int ggml_hip_moe_cache_pin_host(const ggml_hip_moe_tensor *t);
+
+/* ---------------------------------------------------------------------
+ * Companion entry points of the same path
+ * --------------------------------------------------------------------- */
+
+/* The same GEMV for experts that already live in device memory (no table
+ * registration, no stats): the upstream mul_mat_vec_q MoE call that the
+ * reference's intercept falls through to (patches/apply_patches.py:48-62). */
+int ggml_hip_mul_mat_vec_q_moe(
+        const ggml_hip_moe_tensor *src0, const ggml_hip_moe_fusion *fusion,
+        const void *src1_q8_1, const int32_t *ids_d, float *dst_d,
+        int64_t ne00, int64_t ne01, int64_t ne02, int64_t ne03,
+        int64_t ncols_dst, int64_t s01, int64_t s02, int64_t s03,
+        int64_t nchannels_y, int64_t nchannels_dst,
+        int64_t stride_col_y, int64_t stride_col_dst,
+        int64_t stride_channel_y, int64_t stride_channel_dst,
+        int64_t ids_stride, void *stream);
+
+/* Both GEMV entry points with an explicit activation format
+ * (GGML_HIP_MOE_ACT_*).  use_cache = 1 takes the cache path (src0 must satisfy
+ * ggml_hip_moe_cache_wants), 0 the device-resident path.  With
+ * GGML_HIP_MOE_ACT_Q8_K the activation strides count q8_K blocks (256 values). */
+int ggml_hip_moe_mul_mat_vec_ex(
+        int use_cache, int act_format,
+        const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *gate_host,
+        const ggml_hip_moe_fusion *fusion,
+        const void *src1, const int32_t *ids_d, float *dst_d,
+        int64_t ne00, int64_t ne01, int64_t ne02,
+        int64_t ncols_dst, int64_t nchannels_y, int64_t nchannels_dst,
+        int64_t stride_col_y, int64_t stride_col_dst,
+        int64_t stride_channel_y, int64_t stride_channel_dst,
+        int64_t ids_stride, void *stream);
+
+/* q8_1 activation quantizer with ggml-CUDA quantize_q8_1 semantics (the
+ * producer of src1_q8_1, patches/apply_patches.py:52): nrows rows of k fp32
+ * values (x row stride x_stride floats) -> nrows rows of k/32 q8_1 blocks
+ * (y row stride y_stride blocks).  k % 32 == 0. */
+int ggml_hip_quantize_q8_1(const float *x, void *y, int64_t k, int64_t nrows,
+                           int64_t x_stride, int64_t y_stride, void *stream);
+
+/* ggml-CPU activation quantizers on the GPU: q8_K (quantize_row_q8_K_ref,
+ * patches/trace-hook/ggml-cpu.c:308-340 vec_dot_type) into q8_K blocks, and
+ * q8_0 (quantize_row_q8_0_ref, :249-274) written in q8_1 layout (s = 0). */
+int ggml_hip_quantize_q8_K(const float *x, void *y, int64_t k, int64_t nrows,
+                           int64_t x_stride, int64_t y_stride, void *stream);
+int ggml_hip_quantize_q8_0_as_q8_1(const float *x, void *y, int64_t k, int64_t nrows,
+                                   int64_t x_stride, int64_t y_stride, void *stream);
+
+/* ---------------------------------------------------------------------
+ * Configuration, introspection and teardown (the reference reads env vars
+ * once and never frees; kernels/moe-cache.cu:315-363)
+ * --------------------------------------------------------------------- */
+
+typedef struct ggml_hip_moe_config {
+    int32_t     enabled;        /* 1 / 0 */
+    int32_t     slots;          /* pool slots per expert tensor; < 0: every expert */
+    double      budget_gb;      /* total pool budget in GiB; <= 0: free HBM minus margin */
+    double      margin_gb;      /* HBM kept free at registration (reference: 2 GiB) */
+    const char *seed_path;      /* seed file; NULL or "": none */
+    int32_t     max_promotions; /* per step (reference: 48) */
+    int32_t     verbose;        /* registration / step lines on stderr */
+} ggml_hip_moe_config;
+
+/* Replaces the env-derived settings; must be called before the first registration. */
+int ggml_hip_moe_cache_configure(const ggml_hip_moe_config *cfg);
+/* Current settings (after env parsing). */
+int ggml_hip_moe_cache_get_config(ggml_hip_moe_config *out);
+
+typedef struct ggml_hip_moe_entry_info {
+    int32_t  id;             /* cache id (registration order) */
+    int32_t  type;
+    int32_t  n_experts;
+    int32_t  n_slots;
+    uint64_t expert_bytes;
+    int32_t  n_resident;     /* occupied slots */
+    uint32_t stamps_clock;
+} ggml_hip_moe_entry_info;
+
+/* Number of registered tensors. */
+int ggml_hip_moe_cache_num_entries(void);
+/* Info of entry `id`. */
+int ggml_hip_moe_cache_entry_info(int32_t id, ggml_hip_moe_entry_info *out);
+/* slot_of[n_experts] (-1 = cold) and expert_of[n_slots] (-1 = free) of entry `id`. */
+int ggml_hip_moe_cache_entry_slots(int32_t id, int32_t *slot_of, int32_t n_experts, int32_t *expert_of, int32_t n_slots);
+/* Host mirror of the pointer table of entry `id`, decoded: for expert e,
+ * out[e] = slot (>= 0, LSB=0 entry into the pool) or -1 (LSB=1 entry to host memory). */
+int ggml_hip_moe_cache_entry_table(int32_t id, int32_t *out, int32_t n_experts);
+/* Raw device table / stamp array addresses of entry `id` (for device-side checks). */
+int ggml_hip_moe_cache_entry_device(int32_t id, void **d_tbl, void **d_stamps, void **pool);
+/* Device addresses of the global stats words and the LRU clock. */
+int ggml_hip_moe_cache_device_globals(void **d_stats, void **d_clock);
+/* Copies the first n_words device stats words ([0] misses, [1] hits, [2..] miss
+ * log) to out, ordered after all work on `stream`, and waits for the copy. */
+int ggml_hip_moe_cache_stats_snapshot(uint32_t *out, int32_t n_words, void *stream);
+/* Copies entry `id`'s device stamp array (n >= n_experts) to out, as above. */
+int ggml_hip_moe_cache_stamps_snapshot(int32_t id, uint32_t *out, int32_t n, void *stream);
+
+typedef struct ggml_hip_moe_totals {
+    uint64_t steps, hits, misses, promotions, evictions;
+    uint32_t clock;
+    uint32_t last_step_misses, last_step_hits;
+    uint32_t admission_size;
+} ggml_hip_moe_totals;
+int ggml_hip_moe_cache_totals(ggml_hip_moe_totals *out);
+
+/* Frees every pool/table/stat allocation and forgets all registrations
+ * (the reference has no teardown). */
+int ggml_hip_moe_cache_reset(void);
+
+/* Text of the last error on this thread. */
+const char *ggml_hip_moe_last_error(void);
+
+/* Library version string. */
+const char *ggml_hip_moe_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GGML_HIP_MOE_CACHE_H */

@@ -1,0 +1,194 @@
+"""CPU: the product's registry / recorder contract / LRU step code (mc_host.cpp),
+linked against the test-only simulated device, driven through the C ABI and
+checked step by step against oracle/cache_model.py."""
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import cache_scenario as S
+from oracle.cache_model import CacheModel
+
+ROOT = Path(__file__).resolve().parent.parent
+SIM = ROOT / "tests" / "native" / "_build" / "libmc_hostsim.so"
+SEED_FIXTURE = ROOT / "tests" / "golden" / "moe_seed.txt"
+
+
+@pytest.fixture(scope="module")
+def sim(mc):
+    if not SIM.exists():
+        import importlib.util
+        spec = importlib.util.spec_from_file_location("mc_build", ROOT / "a6000-custom-kernels_amd" / "build.py")
+        b = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(b)
+        b.build_hostsim()
+    lib = mc.bind(SIM)
+    lib.mc_sim_host_alloc.restype, lib.mc_sim_host_alloc.argtypes = C.c_void_p, [C.c_uint64]
+    lib.mc_sim_plain_alloc.restype, lib.mc_sim_plain_alloc.argtypes = C.c_void_p, [C.c_uint64]
+    lib.mc_sim_dev_alloc.restype, lib.mc_sim_dev_alloc.argtypes = C.c_void_p, [C.c_uint64]
+    lib.mc_sim_set_mem_info.argtypes = [C.c_uint64, C.c_uint64]
+    lib.mc_sim_fail_alloc_after.argtypes = [C.c_int]
+    lib.mc_sim_counters.argtypes = [C.c_void_p]
+    return lib
+
+
+class SimBackend:
+    def __init__(self, lib):
+        self.lib = lib
+        self.stream = C.c_void_p(0)
+
+    def host_tensor(self, nbytes, role):
+        p = self.lib.mc_sim_host_alloc(nbytes)
+        assert p
+        return p, p
+
+    def ids_buffer(self, n_tok, n_used):
+        self.ids = np.zeros((n_tok, n_used), np.int32)
+
+        def setter(ids):
+            self.ids[:] = ids
+        return self.ids.ctypes.data, setter
+
+    def act_buffer(self, n_tok, K):
+        self.y = np.zeros(n_tok * K, np.uint8)
+        return self.y.ctypes.data
+
+    def dst_buffer(self, n_tok, n_used, R):
+        self.dst = np.zeros(n_tok * n_used * R, np.float32)
+        return self.dst.ctypes.data
+
+
+@pytest.mark.parametrize("slots,steps,n_tok,n_used,max_promo,rseed", [
+    (5, 30, 2, 4, 48, 1), (3, 25, 4, 8, 2, 2), (16, 10, 1, 8, 48, 3), (0, 8, 2, 4, 48, 4), (1, 40, 3, 6, 5, 5)])
+def test_sim_scenario_matches_model(sim, mc, tmp_path, slots, steps, n_tok, n_used, max_promo, rseed):
+    seed_path = str(tmp_path / "seed.txt")
+    with open(seed_path, "w") as f:
+        f.write(f"{S.UP_NAME} 4,4,1,2\n{S.GATE_NAME} 9,15,17,-1\n")
+    sim.mc_sim_set_mem_info(64 << 30, 64 << 30)
+    model, keep = S.run_scenario(mc, sim, SimBackend(sim), n_experts=16, R=8, K=256, wtype=10, slots=slots,
+                                 steps=steps, n_tok=n_tok, n_used=n_used, seed_path=seed_path, free_bytes=64 << 30,
+                                 max_promotions=max_promo, rng_seed=rseed)
+    if slots:
+        assert model.promotions > 0
+
+
+def test_sim_budget_and_free_memory_clamp(sim, mc):
+    """slots = min(SLOTS, budget_left/eb, (free - margin)/eb, n_experts) (kernels/moe-cache.cu:542-561)."""
+    be = SimBackend(sim)
+    K, R, n = 256, 8, 64
+    eb = mc.row_bytes(mc.Q2_K, K) * R          # 672 bytes
+    cfg = mc.Config()
+    cfg.enabled, cfg.slots, cfg.budget_gb, cfg.margin_gb, cfg.seed_path, cfg.max_promotions = 1, 40, 30 * eb / (1 << 30), 0.0, None, 48
+    assert sim.ggml_hip_moe_cache_reset() == 0
+    assert sim.ggml_hip_moe_cache_configure(C.byref(cfg)) == 0
+    sim.mc_sim_set_mem_info(12 * eb, 1 << 30)    # free memory binds for the 2nd tensor
+    keep = []
+    ids_p, set_ids = be.ids_buffer(1, 2)
+    set_ids(np.array([[0, 1]], np.int32))
+    got = []
+    for i in range(3):
+        p = be.host_tensor(eb * n, "up")[0]
+        t = mc.make_tensor(mc.Q2_K, K, R, n, p, name=f"t{i}", keep=keep)
+        rc = sim.ggml_hip_moe_cache_mul_mat_vec_q(C.byref(t), None, None, be.act_buffer(1, K), ids_p,
+                                                   be.dst_buffer(1, 2, R), K, R, n, 1, 1, 1, eb, eb * n, 1, 2, 8, 2 * R,
+                                                   8, R, 2, be.stream)
+        assert rc == 0, sim.ggml_hip_moe_last_error()
+        info = mc.EntryInfo()
+        sim.ggml_hip_moe_cache_entry_info(i, C.byref(info))
+        got.append(info.n_slots)
+    # tensor 0: min(40, budget 30, free 12) = 12; tensor 1: min(40, 18, 12) = 12; tensor 2: min(40, 6, 12) = 6
+    model = CacheModel(slots=40, budget_bytes=int(30 * eb / (1 << 30) * (1 << 30)), margin_bytes=0)
+    want = [model.register(i, f"t{i}", n, eb, 12 * eb).n_slots for i in range(3)]
+    assert got == want == [12, 12, 6]
+    sim.mc_sim_set_mem_info(64 << 30, 64 << 30)
+
+
+def test_sim_alloc_failure_is_an_error_not_an_abort(sim, mc):
+    be = SimBackend(sim)
+    assert sim.ggml_hip_moe_cache_reset() == 0
+    cfg = mc.Config()
+    cfg.enabled, cfg.slots, cfg.budget_gb, cfg.margin_gb, cfg.seed_path, cfg.max_promotions = 1, 4, 0.0, 0.0, None, 48
+    assert sim.ggml_hip_moe_cache_configure(C.byref(cfg)) == 0
+    K, R, n = 256, 8, 8
+    eb = mc.row_bytes(mc.Q2_K, K) * R
+    keep = []
+    p = be.host_tensor(eb * n, "up")[0]
+    t = mc.make_tensor(mc.Q2_K, K, R, n, p, name="x", keep=keep)
+    ids_p, set_ids = be.ids_buffer(1, 2)
+    set_ids(np.array([[0, 1]], np.int32))
+    sim.mc_sim_fail_alloc_after(3)   # stats, pinned stats, clock succeed; the table allocation fails
+    rc = sim.ggml_hip_moe_cache_mul_mat_vec_q(C.byref(t), None, None, be.act_buffer(1, K), ids_p, be.dst_buffer(1, 2, R),
+                                               K, R, n, 1, 1, 1, eb, eb * n, 1, 2, 8, 2 * R, 8, R, 2, be.stream)
+    sim.mc_sim_fail_alloc_after(-1)
+    assert rc < 0
+    assert b"alloc" in sim.ggml_hip_moe_last_error()
+    assert sim.ggml_hip_moe_cache_num_entries() == 0
+
+
+def test_sim_rejects_unsupported(sim, mc):
+    be = SimBackend(sim)
+    assert sim.ggml_hip_moe_cache_reset() == 0
+    cfg = mc.Config()
+    cfg.enabled, cfg.slots, cfg.budget_gb, cfg.margin_gb, cfg.seed_path, cfg.max_promotions = 1, 4, 0.0, 0.0, None, 48
+    assert sim.ggml_hip_moe_cache_configure(C.byref(cfg)) == 0
+    keep = []
+    p = be.host_tensor(1 << 16, "up")[0]
+    t = mc.make_tensor(mc.Q2_K, 256, 8, 8, p, name="x", keep=keep)
+    assert sim.ggml_hip_moe_cache_wants(C.byref(t)) == 1
+    t.type = 3                                     # Q4_1: not on the path
+    assert sim.ggml_hip_moe_cache_wants(C.byref(t)) == 0
+    t.type = mc.Q2_K
+    t.nb[1] += 4                                   # non-contiguous rows
+    assert sim.ggml_hip_moe_cache_wants(C.byref(t)) == 0
+    t = mc.make_tensor(mc.Q2_K, 256, 8, 8, sim.mc_sim_plain_alloc(1 << 16), name="y", keep=keep)
+    assert sim.ggml_hip_moe_cache_wants(C.byref(t)) == 0       # not GPU-readable host memory
+    assert sim.ggml_hip_moe_cache_pin_host(C.byref(t)) == 0    # registration not allowed by default
+    t = mc.make_tensor(mc.Q2_K, 256, 8, 8, sim.mc_sim_dev_alloc(1 << 16), name="z", keep=keep)
+    assert sim.ggml_hip_moe_cache_wants(C.byref(t)) == 0       # device memory
+    # an unsupported type through the GEMV entry is an error code, not an abort
+    t = mc.make_tensor(mc.Q2_K, 256, 8, 8, p, name="x", keep=keep)
+    t.type = 3
+    ids_p, set_ids = be.ids_buffer(1, 2)
+    rc = sim.ggml_hip_moe_cache_mul_mat_vec_q(C.byref(t), None, None, be.act_buffer(1, 256), ids_p, be.dst_buffer(1, 2, 8),
+                                               256, 8, 8, 1, 1, 1, 0, 0, 1, 2, 8, 16, 8, 8, 2, be.stream)
+    assert rc < 0
+
+
+def test_sim_disabled_by_default(sim, mc):
+    assert sim.ggml_hip_moe_cache_reset() == 0
+    cfg = mc.Config()
+    cfg.enabled = 0
+    assert sim.ggml_hip_moe_cache_configure(C.byref(cfg)) == 0
+    assert sim.ggml_hip_moe_cache_enabled() == 0
+    assert sim.ggml_hip_moe_cache_step(None) == 0      # no-op
+    assert sim.ggml_hip_moe_cache_active() == 0
+
+
+def test_sim_seed_fixture_registration(sim, mc):
+    """Registration with the reference's own seed file: slots 0..k-1 follow the file's order."""
+    from oracle.cache_model import parse_seed_file
+    seed = parse_seed_file(SEED_FIXTURE)
+    name = "blk.47.ffn_gate_exps.weight"
+    be = SimBackend(sim)
+    assert sim.ggml_hip_moe_cache_reset() == 0
+    cfg = mc.Config()
+    cfg.enabled, cfg.slots, cfg.budget_gb, cfg.margin_gb, cfg.max_promotions = 1, 100, 0.0, 0.0, 48
+    sp = str(SEED_FIXTURE).encode()
+    cfg.seed_path = sp
+    assert sim.ggml_hip_moe_cache_configure(C.byref(cfg)) == 0
+    sim.mc_sim_set_mem_info(64 << 30, 64 << 30)
+    K, R, n = 256, 2, 512
+    eb = mc.row_bytes(mc.Q2_K, K) * R
+    keep = []
+    p = be.host_tensor(eb * n, "up")[0]
+    t = mc.make_tensor(mc.Q2_K, K, R, n, p, name=name, keep=keep)
+    ids_p, set_ids = be.ids_buffer(1, 1)
+    set_ids(np.array([[0]], np.int32))
+    rc = sim.ggml_hip_moe_cache_mul_mat_vec_q(C.byref(t), None, None, be.act_buffer(1, K), ids_p, be.dst_buffer(1, 1, R),
+                                               K, R, n, 1, 1, 1, eb, eb * n, 1, 1, 8, R, 8, R, 1, be.stream)
+    assert rc == 0, sim.ggml_hip_moe_last_error()
+    expert_of = np.empty(100, np.int32)
+    assert sim.ggml_hip_moe_cache_entry_slots(0, None, 0, expert_of.ctypes.data, 100) == 0
+    assert expert_of[:5].tolist() == [333, 183, 357, 241, 146]
+    assert expert_of.tolist() == seed[name][:100]
