@@ -33,6 +33,7 @@ struct Device {
     virtual int register_host(void *base, size_t n) = 0;
     virtual int launch_gemv(const GemvArgs &a, int tw, int ts, int act, void *stream) = 0;
     virtual int launch_quantize(int kind, const QuantArgs &q, void *stream) = 0;
+    virtual int launch_combine(const CombineArgs &c, void *stream) = 0;
     virtual const char *error_string(int code) = 0;
 };
 

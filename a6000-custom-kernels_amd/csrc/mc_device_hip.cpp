@@ -7,6 +7,7 @@ namespace mc {
 
 int launch_gemv(GemvArgs a, int tw, int ts, int act, void *stream);   // mc_kernels.hip
 int launch_quantize(int kind, const QuantArgs &q, void *stream);      // mc_kernels.hip
+int launch_combine(const CombineArgs &c, void *stream);               // mc_kernels.hip
 
 namespace {
 
@@ -50,6 +51,7 @@ struct HipDevice final : Device {
         return mc::launch_gemv(a, tw, ts, act, s);
     }
     int launch_quantize(int kind, const QuantArgs &q, void *s) override { return mc::launch_quantize(kind, q, s); }
+    int launch_combine(const CombineArgs &c, void *s) override { return mc::launch_combine(c, s); }
     const char *error_string(int code) override { return hipGetErrorString((hipError_t) code); }
 };
 

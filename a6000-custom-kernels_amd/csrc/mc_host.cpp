@@ -745,6 +745,34 @@ int ggml_hip_quantize_q8_0_as_q8_1(const float *x, void *y, int64_t k, int64_t n
     return quantize_common(2, x, y, k, nrows, x_stride, y_stride, stream);
 }
 
+int ggml_hip_moe_combine_q8_1(const float *o, int64_t o_stride, const float *w, int32_t n_used, const float *shared,
+                              int64_t shared_stride, const float *residual, float *x_out, void *y_q8_1, int64_t y_stride,
+                              int64_t k, int64_t n_tok, int32_t rms_norm, float eps, void *stream) {
+    if (!y_q8_1 || (n_used > 0 && (!o || !w))) return fail(E_INVALID, "combine: null argument");
+    if (k <= 0 || k % 32 || k > 8192 || n_used < 0 || n_used > 16 || n_tok < 0 || (n_used > 0 && o_stride < k) ||
+        (shared && shared_stride < k) || y_stride < k / 32)
+        return fail(E_INVALID, "combine: bad shape");
+    if ((uintptr_t) y_q8_1 & 3u) return fail(E_INVALID, "combine: misaligned output");
+    CombineArgs c;
+    c.o = o;
+    c.o_stride = o_stride;
+    c.w = w;
+    c.shared = shared;
+    c.shared_stride = shared_stride;
+    c.residual = residual;
+    c.x_out = x_out;
+    c.y = (uint8_t *) y_q8_1;
+    c.y_stride = y_stride * 36;
+    c.k = k;
+    c.n_used = n_used;
+    c.n_tok = (int32_t) n_tok;
+    c.rms_norm = rms_norm ? 1 : 0;
+    c.eps = eps;
+    const int rc = dev()->launch_combine(c, stream);
+    if (rc) return dev_err(rc, "combine launch");
+    return 0;
+}
+
 int ggml_hip_moe_cache_configure(const ggml_hip_moe_config *cfg) {
     if (!cfg) return fail(E_INVALID, "configure: null config");
     std::lock_guard<std::mutex> lock(g_mutex);

@@ -125,6 +125,23 @@ struct QuantArgs {
     int64_t y_stride;   // bytes between rows
 };
 
+struct CombineArgs {
+    const float *o;          // [n_tok][n_used][o_stride] routed expert outputs
+    int64_t o_stride;        // floats between picks
+    const float *w;          // [n_tok][n_used] router weights
+    const float *shared;     // [n_tok][shared_stride] shared-expert output, or null
+    int64_t shared_stride;
+    const float *residual;   // [n_tok][k], or null
+    float *x_out;            // [n_tok][k], or null
+    uint8_t *y;              // q8_1 rows of the combined vector
+    int64_t y_stride;        // bytes between rows
+    int64_t k;
+    int32_t n_used;
+    int32_t n_tok;
+    int32_t rms_norm;        // 1: quantize x / rms(x) (weightless RMSNorm), 0: quantize x
+    float eps;
+};
+
 }  // namespace mc
 
 #endif

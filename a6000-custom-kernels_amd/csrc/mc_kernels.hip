@@ -739,6 +739,79 @@ __global__ __launch_bounds__(64) void mc_quantize_q8_K_kernel(const QuantArgs a)
     if (lane == 0) *(float *) yb = 1.0f / iscale;
 }
 
+// MoE combine + next-layer quantization, one 1024-thread workgroup per token row:
+//   x = residual + shared + sum_j w[j] * o[j]      (j ascending, fmaf), written to x_out;
+//   optional weightless RMSNorm of x (the ffn_norm in front of the next MoE block):
+//     thread t accumulates x[t + 1024 i]^2 with fmaf over i, the 1024 partials are
+//     tree-summed (offsets 512 .. 1), scale = 1 / sqrtf(sum / k + eps);
+//   then q8_1 quantization of x * scale exactly like mc_quantize_q8_1_kernel.
+// This is the weighted sum ggml performs after MUL_MAT_ID (MUL by the router
+// weights, then ADDs) fused with the quantize_q8_1 of the next GEMV's input.
+// Every thread issues all of its loads before the first use (the row is small
+// and latency, not bandwidth, bounds this kernel).
+constexpr int COMBINE_MAX_K = 8192;
+constexpr int COMBINE_THREADS = 1024;
+constexpr int COMBINE_MAX_USED = 16;
+
+__global__ __launch_bounds__(COMBINE_THREADS) void mc_combine_q8_1_kernel(const CombineArgs a) {
+    __shared__ float xs[COMBINE_MAX_K];
+    __shared__ float part[COMBINE_THREADS];
+    const int64_t t = blockIdx.x;
+    const int tid = threadIdx.x;
+    constexpr int PER = COMBINE_MAX_K / COMBINE_THREADS;
+    float wj[COMBINE_MAX_USED];
+#pragma unroll
+    for (int j = 0; j < COMBINE_MAX_USED; ++j) wj[j] = j < a.n_used ? a.w[t * a.n_used + j] : 0.0f;
+    float ss = 0.0f;
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+        const int64_t i = tid + (int64_t) r * COMBINE_THREADS;
+        if (i >= a.k) break;
+        float ov[COMBINE_MAX_USED];
+#pragma unroll
+        for (int j = 0; j < COMBINE_MAX_USED; ++j) ov[j] = j < a.n_used ? a.o[(t * a.n_used + j) * a.o_stride + i] : 0.0f;
+        float x = a.residual ? a.residual[t * a.k + i] : 0.0f;
+        if (a.shared) x += a.shared[t * a.shared_stride + i];
+#pragma unroll
+        for (int j = 0; j < COMBINE_MAX_USED; ++j)
+            if (j < a.n_used) x = fmaf(wj[j], ov[j], x);
+        if (a.x_out) a.x_out[t * a.k + i] = x;
+        xs[i] = x;
+        ss = fmaf(x, x, ss);
+    }
+    float scale = 1.0f;
+    if (a.rms_norm) {
+        part[tid] = ss;
+        __syncthreads();
+        for (int off = COMBINE_THREADS / 2; off > 0; off >>= 1) {
+            if (tid < off) part[tid] += part[tid + off];
+            __syncthreads();
+        }
+        scale = 1.0f / sqrtf(part[0] / (float) a.k + a.eps);
+    } else {
+        __syncthreads();
+    }
+    const int grp = tid >> 5, l = tid & 31;
+    for (int64_t b = grp; b < a.k / 32; b += COMBINE_THREADS / 32) {
+        float x;
+        {
+#pragma clang fp contract(off)
+            x = xs[b * 32 + l] * scale;
+        }
+        float amax = fabsf(x), sum = x;
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) {
+            amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+            sum += __shfl_xor(sum, off, 32);
+        }
+        const float d = amax / 127.0f;
+        const int8_t q = amax == 0.0f ? (int8_t) 0 : (int8_t) roundf(x / d);
+        uint8_t *yb = a.y + t * a.y_stride + b * 36;
+        yb[4 + l] = (uint8_t) q;
+        if (l == 0) *(u32 *) yb = (u32) f2h_bits(d) | ((u32) f2h_bits(sum) << 16);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // host-side launchers
 // ---------------------------------------------------------------------------
@@ -814,6 +887,14 @@ int launch_gemv(GemvArgs a, int tw, int ts, int act, void *stream) {
         case T_Q6_K: return (int) launch_act<T_Q6_K>(a, ts, act, s);
         default: return (int) hipErrorInvalidValue;
     }
+}
+
+int launch_combine(const CombineArgs &c, void *stream) {
+    if (c.n_tok <= 0 || c.k <= 0) return (int) hipSuccess;
+    if (c.k > COMBINE_MAX_K || c.n_used > COMBINE_MAX_USED) return (int) hipErrorInvalidValue;
+    hipLaunchKernelGGL(mc_combine_q8_1_kernel, dim3((unsigned) c.n_tok), dim3(COMBINE_THREADS), 0,
+                       (hipStream_t) stream, c);
+    return (int) hipGetLastError();
 }
 
 int launch_quantize(int kind, const QuantArgs &q, void *stream) {

@@ -1,0 +1,195 @@
+"""Synthetic multi-layer MoE decode step on the gfx950 GEMV (batch-1 decode).
+
+Per layer, for one token (the op sequence of a ggml MoE FFN block):
+  1. gate/up MUL_MAT_ID over the routed experts, fused SwiGLU, with the shared
+     expert's gate/up in the same launch          -> h[0..n_used)   and h[n_used]
+  2. q8_1 quantization of the n_used+1 GLU rows    -> hq
+  3. down MUL_MAT_ID (one activation row per slot), shared expert's down in the
+     same launch                                    -> o[0..n_used) and o_sh
+  4. combine x' = x + o_sh + sum_j w_j o_j, fused with the q8_1 quantization of
+     x' for the next layer's gate/up launch.
+Every launch goes through the C ABI (include/ggml_hip_moe_cache.h); one token is
+captured once into a hipGraph and replayed, with routing ids and router
+weights copied into fixed device buffers before each replay.
+
+Weights are random valid quantized blocks (uniform codes and scale bits, fp16
+block scales set to finite values of realistic magnitude) generated on the GPU:
+the GEMV's speed does not depend on the values; numerics are covered by the
+parity tests against the CPU oracle.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+import numpy as np
+
+from . import (ACT_Q8_1, BLOCK, GLU_SWIGLU, KQUANTS, Q2_K, Q3_K, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0, check,
+               lib, make_fusion, make_tensor, row_bytes)
+
+# byte offsets of the fp16 block-scale fields per type, and the value written there
+_SCALE_FIELDS = {
+    Q2_K: ((80, 2e-3), (82, 2e-3)),
+    Q3_K: ((108, 2e-4),),
+    Q4_K: ((0, 4e-5), (2, 4e-5)),
+    Q5_K: ((0, 2e-5), (2, 2e-5)),
+    Q6_K: ((208, 5e-6),),
+    Q4_0: ((0, 2e-3),),
+    Q5_0: ((0, 1e-3),),
+    Q8_0: ((0, 2e-4),),
+}
+
+
+def random_expert_tensor(torch, wtype, n_experts, rows, k, gen, device="cuda"):
+    """uint8 [n_experts, rows, row_bytes] of valid random blocks of `wtype`."""
+    rb = row_bytes(wtype, k)
+    t = torch.randint(0, 256, (n_experts, rows, rb), dtype=torch.uint8, device=device, generator=gen)
+    bb = BLOCK[wtype][1]
+    blocks = t.view(n_experts, rows, rb // bb, bb)
+    for off, val in _SCALE_FIELDS[wtype]:
+        h = np.array([val], dtype=np.float16).view(np.uint8)
+        blocks[..., off] = int(h[0])
+        blocks[..., off + 1] = int(h[1])
+    return t
+
+
+class Layer:
+    pass
+
+
+class MoeDecodeModel:
+    def __init__(self, torch, n_layers=48, n_experts=512, hidden=4096, ffn=768, n_used=8, wtype=Q2_K,
+                 sh_type=Q4_K, seed=0, device="cuda", residual=True):
+        self.torch = torch
+        self.L, self.E, self.H, self.F, self.U = n_layers, n_experts, hidden, ffn, n_used
+        self.wtype, self.sh_type = wtype, sh_type
+        self.residual = residual
+        self.eps = 1e-6
+        gen = torch.Generator(device=device)
+        gen.manual_seed(seed)
+        self.layers = []
+        keep = []
+        for _ in range(n_layers):
+            ly = Layer()
+            ly.gate = random_expert_tensor(torch, wtype, n_experts, ffn, hidden, gen, device)
+            ly.up = random_expert_tensor(torch, wtype, n_experts, ffn, hidden, gen, device)
+            ly.down = random_expert_tensor(torch, wtype, n_experts, hidden, ffn, gen, device)
+            ly.sh_gate = random_expert_tensor(torch, sh_type, 1, ffn, hidden, gen, device)[0]
+            ly.sh_up = random_expert_tensor(torch, sh_type, 1, ffn, hidden, gen, device)[0]
+            ly.sh_down = random_expert_tensor(torch, sh_type, 1, hidden, ffn, gen, device)[0]
+            ly.t_up = make_tensor(wtype, hidden, ffn, n_experts, ly.up.data_ptr(), keep=keep)
+            ly.t_down = make_tensor(wtype, ffn, hidden, n_experts, ly.down.data_ptr(), keep=keep)
+            self.layers.append(ly)
+        self._keep = keep
+        f32, u8, i32 = torch.float32, torch.uint8, torch.int32
+        self.x = torch.zeros((1, hidden), dtype=f32, device=device)          # residual stream
+        self.x_next = torch.zeros((1, hidden), dtype=f32, device=device)
+        self.y = torch.zeros((1, hidden // 32 * 36), dtype=u8, device=device)
+        self.h = torch.zeros((n_used + 1, ffn), dtype=f32, device=device)   # row n_used: shared expert
+        self.hq = torch.zeros((n_used + 1, ffn // 32 * 36), dtype=u8, device=device)
+        self.o = torch.zeros((n_used, hidden), dtype=f32, device=device)
+        self.o_sh = torch.zeros((1, hidden), dtype=f32, device=device)
+        self.ids = torch.zeros((n_layers, 1, n_used), dtype=i32, device=device)
+        self.w = torch.zeros((n_layers, 1, n_used), dtype=f32, device=device)
+        for ly in self.layers:
+            ly.f_gu = make_fusion(gate=ly.gate, glu_op=GLU_SWIGLU, shared_up=ly.sh_up, shared_gate=ly.sh_gate,
+                                  shared_dst=self.h[n_used:], shared_type=sh_type)
+            ly.f_dn = make_fusion(shared_up=ly.sh_down, shared_dst=self.o_sh, shared_type=sh_type,
+                                  shared_src1=self.hq[n_used:], shared_stride_col_y=ffn // 32)
+        self.graph = None
+
+    # bytes one token reads by definition (unique expert matrices + shared + activations + outputs)
+    def bytes_per_token(self):
+        H, F, U = self.H, self.F, self.U
+        eb_gu = row_bytes(self.wtype, H) * F
+        eb_dn = row_bytes(self.wtype, F) * H
+        sh = row_bytes(self.sh_type, H) * F * 2 + row_bytes(self.sh_type, F) * H
+        act = H // 32 * 36 + (U + 1) * F // 32 * 36
+        out = (U + 1) * F * 4 + (U + 1) * H * 4
+        return self.L * (U * (2 * eb_gu + eb_dn) + sh + act + out)
+
+    def gate_up_bytes(self):
+        H, F, U = self.H, self.F, self.U
+        return (U * 2 * row_bytes(self.wtype, H) * F + 2 * row_bytes(self.sh_type, H) * F
+                + H // 32 * 36 + (U + 1) * F * 4)
+
+    def down_bytes(self):
+        H, F, U = self.H, self.F, self.U
+        return U * row_bytes(self.wtype, F) * H + row_bytes(self.sh_type, F) * H + (U + 1) * F // 32 * 36 + (U + 1) * H * 4
+
+    def _stream(self):
+        return C.c_void_p(self.torch.cuda.current_stream().cuda_stream)
+
+    def launch_gate_up(self, l, s=None):
+        ly = self.layers[l]
+        s = s or self._stream()
+        H, F, U = self.H, self.F, self.U
+        check(lib().ggml_hip_moe_mul_mat_vec_ex(0, ACT_Q8_1, C.byref(ly.t_up), None, C.byref(ly.f_gu),
+                                                self.y.data_ptr(), self.ids[l].data_ptr(), self.h.data_ptr(),
+                                                H, F, self.E, 1, 1, U, H // 32, U * F, H // 32, F, U, s), "gate_up")
+
+    def launch_down(self, l, s=None):
+        ly = self.layers[l]
+        s = s or self._stream()
+        H, F, U = self.H, self.F, self.U
+        check(lib().ggml_hip_moe_mul_mat_vec_ex(0, ACT_Q8_1, C.byref(ly.t_down), None, C.byref(ly.f_dn),
+                                                self.hq.data_ptr(), self.ids[l].data_ptr(), self.o.data_ptr(),
+                                                F, H, self.E, 1, U, U, (U + 1) * F // 32, U * H, F // 32, H, U, s),
+              "down")
+
+    def launch_layer(self, l, s=None):
+        s = s or self._stream()
+        H, F, U = self.H, self.F, self.U
+        self.launch_gate_up(l, s)
+        check(lib().ggml_hip_quantize_q8_1(self.h.data_ptr(), self.hq.data_ptr(), F, U + 1, F, F // 32, s), "quantize h")
+        self.launch_down(l, s)
+        src, dst = (self.x, self.x_next) if l % 2 == 0 else (self.x_next, self.x)
+        check(lib().ggml_hip_moe_combine_q8_1(self.o.data_ptr(), H, self.w[l].data_ptr(), U, self.o_sh.data_ptr(), H,
+                                              src.data_ptr() if self.residual else None, dst.data_ptr(),
+                                              self.y.data_ptr(), H // 32, H, 1, 1, self.eps, s), "combine")
+
+    def launch_token(self):
+        """One token through every layer; the token's input and output are in self.x."""
+        s = self._stream()
+        # RMS-normalized q8_1 of the input (the ffn_norm in front of the first MoE block)
+        check(lib().ggml_hip_moe_combine_q8_1(None, 0, None, 0, None, 0, self.x.data_ptr(), None, self.y.data_ptr(),
+                                              self.H // 32, self.H, 1, 1, self.eps, s), "quantize x")
+        for l in range(self.L):
+            self.launch_layer(l, s)
+        if self.L % 2 == 1:
+            self.x.copy_(self.x_next)
+
+    def set_routing(self, ids, w):
+        """ids: int32 [L, n_used], w: fp32 [L, n_used] (device or host tensors)."""
+        self.ids.view(self.L, self.U).copy_(ids, non_blocking=True)
+        self.w.view(self.L, self.U).copy_(w, non_blocking=True)
+
+    def capture(self):
+        torch = self.torch
+        self.launch_token()                      # first use builds every device table
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                self.launch_token()
+        torch.cuda.current_stream().wait_stream(s)
+        self.graph = g
+        return g
+
+    def replay(self):
+        self.graph.replay()
+
+
+def make_routing(n_tokens, n_layers, n_experts, n_used, seed=0):
+    """Uniform top-n_used ids without replacement and softmax router weights over N(0,1) logits."""
+    rng = np.random.default_rng(seed)
+    ids = np.empty((n_tokens, n_layers, n_used), np.int32)
+    for t in range(n_tokens):
+        for l in range(n_layers):
+            ids[t, l] = rng.choice(n_experts, size=n_used, replace=False)
+    logits = rng.standard_normal((n_tokens, n_layers, n_used)).astype(np.float32)
+    w = np.exp(logits - logits.max(-1, keepdims=True))
+    w /= w.sum(-1, keepdims=True)
+    return ids, w.astype(np.float32)

@@ -916,6 +916,38 @@ int or_cpu_mul_mat_id_f32(int type, int64_t ne00, int64_t ne01, int32_t n_as,
     return 0;
 }
 
+/* The combine is written the way the GPU kernel's 1024 threads split the row so
+ * that the normalization is reproduced bit for bit: thread t owns elements
+ * t, t+1024, ...; its partial sum of squares accumulates with fmaf in that
+ * order; the 1024 partials are tree-summed with offsets 512, 256, ..., 1. */
+#define OR_COMBINE_THREADS 1024
+void or_combine_q8_1(const float *o, int64_t o_stride, const float *w, int32_t n_used, const float *shared,
+                     int64_t shared_stride, const float *residual, float *x_out, void *y, int64_t k, int64_t n_tok,
+                     int32_t rms_norm, float eps) {
+    float *xs = (float *) malloc(sizeof(float) * (size_t) k);
+    for (int64_t t = 0; t < n_tok; ++t) {
+        float part[OR_COMBINE_THREADS];
+        for (int th = 0; th < OR_COMBINE_THREADS; ++th) part[th] = 0.0f;
+        for (int64_t i = 0; i < k; ++i) {
+            float v = residual ? residual[t * k + i] : 0.0f;
+            if (shared) v += shared[t * shared_stride + i];
+            for (int32_t j = 0; j < n_used; ++j) v = fmaf(w[t * n_used + j], o[(t * n_used + j) * o_stride + i], v);
+            if (x_out) x_out[t * k + i] = v;
+            part[i % OR_COMBINE_THREADS] = fmaf(v, v, part[i % OR_COMBINE_THREADS]);
+            xs[i] = v;
+        }
+        float scale = 1.0f;
+        if (rms_norm) {
+            for (int off = OR_COMBINE_THREADS / 2; off > 0; off >>= 1)
+                for (int th = 0; th < off; ++th) part[th] += part[th + off];
+            scale = 1.0f / sqrtf(part[0] / (float) k + eps);
+        }
+        for (int64_t i = 0; i < k; ++i) xs[i] = xs[i] * scale;
+        or_quantize_q8_1(xs, (char *) y + (size_t) t * (size_t) (k / 32) * 36, k);
+    }
+    free(xs);
+}
+
 /* ------------------------------------------------------------------ */
 /* deterministic generators                                            */
 /* ------------------------------------------------------------------ */
