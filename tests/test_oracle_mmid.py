@@ -1,0 +1,94 @@
+"""CPU: pins the oracle's MUL_MAT_ID (ggml-CPU restatement and the fused-op
+variant) against a numpy fp64 evaluation on dequantized operands."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+
+def _deq_experts(t, w, K):
+    n, R, _ = w.shape
+    return O.dequantize(t, w.reshape(n * R, -1), K).reshape(n, R, K).astype(np.float64)
+
+
+@pytest.mark.parametrize("t", O.WEIGHT_TYPES)
+def test_cpu_mul_mat_id_brute_force(t):
+    K, R, n_as, n_tok, n_used = 512, 20, 6, 3, 4
+    w = O.quantize_weights(t, O.fill_normal(10 + t, n_as * R * K, 0, 0.02).reshape(-1, K)).reshape(n_as, R, -1)
+    x = O.fill_normal(20 + t, n_tok * K).reshape(n_tok, K)
+    ids = O.topk_uniform(30 + t, n_as, n_used, n_tok)
+    got = O.cpu_mul_mat_id_f32(wtype=t, K=K, R=R, n_as=n_as, src0=w, src1=x, ids=ids, nthreads=3)
+    wd = _deq_experts(t, w, K)
+    act_t = O.lib().or_act_type(t, O.ACT_CPU)
+    for tok in range(n_tok):
+        aq = O.quantize_act(t, O.ACT_CPU, x[tok])
+        ad = O.dequantize(act_t, aq, K)[0].astype(np.float64)
+        for c in range(n_used):
+            want = wd[ids[tok, c]] @ ad
+            assert np.allclose(got[tok, c], want, rtol=1e-5, atol=1e-6 * np.abs(want).max()), (t, tok, c)
+    # the oracle's threading does not change the result
+    assert np.array_equal(got, O.cpu_mul_mat_id_f32(wtype=t, K=K, R=R, n_as=n_as, src0=w, src1=x, ids=ids, nthreads=1))
+
+
+def test_cpu_mul_mat_id_repeated_expert_and_broadcast_rows():
+    """Two tokens picking the same expert, and src1 with one row per slot (down-projection shape)."""
+    t, K, R, n_as = O.Q4_K, 256, 8, 4
+    w = O.quantize_weights(t, O.fill_normal(5, n_as * R * K, 0, 0.02).reshape(-1, K)).reshape(n_as, R, -1)
+    ids = np.array([[2, 0], [2, 3]], np.int32)
+    x = O.fill_normal(6, 2 * 2 * K).reshape(2, 2, K)             # [tok, slot, K]
+    got = O.cpu_mul_mat_id_f32(wtype=t, K=K, R=R, n_as=n_as, src0=w, src1=x, ids=ids, nthreads=2)
+    wd = _deq_experts(t, w, K)
+    for tok in range(2):
+        for c in range(2):
+            ad = O.dequantize(O.Q8_K, O.quantize_act(t, O.ACT_CPU, x[tok, c]), K)[0].astype(np.float64)
+            assert np.allclose(got[tok, c], wd[ids[tok, c]] @ ad, rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("glu_op", [O.GLU_SWIGLU, O.GLU_GEGLU, O.GLU_REGLU])
+def test_fused_mul_mat_id_post_ops(glu_op):
+    """scale -> bias -> GLU(gate, up) and the shared expert, against numpy on the same activation bytes."""
+    t, st, K, R, n_as, n_tok, n_used = O.Q2_K, O.Q4_K, 512, 12, 5, 2, 3
+    up = O.quantize_weights(t, O.fill_normal(40, n_as * R * K, 0, 0.02).reshape(-1, K)).reshape(n_as, R, -1)
+    gate = O.quantize_weights(t, O.fill_normal(41, n_as * R * K, 0, 0.02).reshape(-1, K)).reshape(n_as, R, -1)
+    shu = O.quantize_weights(st, O.fill_normal(42, R * K, 0, 0.02).reshape(-1, K))
+    shg = O.quantize_weights(st, O.fill_normal(43, R * K, 0, 0.02).reshape(-1, K))
+    x = O.fill_normal(44, n_tok * K).reshape(n_tok, K)
+    ids = O.topk_uniform(45, n_as, n_used, n_tok)
+    rng = np.random.default_rng(46)
+    xb, gb = rng.standard_normal((n_as, R)).astype(np.float32) * 0.1, rng.standard_normal((n_as, R)).astype(np.float32) * 0.1
+    xs, gs = rng.uniform(0.5, 1.5, n_as).astype(np.float32), rng.uniform(0.5, 1.5, n_as).astype(np.float32)
+    act = np.stack([O.quantize_q8_1(r) for r in x]).reshape(n_tok, 1, -1)
+    dst, sh = O.mul_mat_id(wtype=t, K=K, R=R, n_as=n_as, src0=up, gate=gate, ids=ids, act=act, act_kind=O.ACT_Q8_1,
+                           x_bias=xb, gate_bias=gb, x_scale=xs, gate_scale=gs, glu_op=glu_op, sh_type=st, sh_up=shu,
+                           sh_gate=shg)
+    ud, gd = _deq_experts(t, up, K), _deq_experts(t, gate, K)
+    sud, sgd = O.dequantize(st, shu, K).astype(np.float64), O.dequantize(st, shg, K).astype(np.float64)
+    sig = lambda z: 1 / (1 + np.exp(-z))
+    f = {O.GLU_SWIGLU: lambda g, u: u * g * sig(g),
+         O.GLU_GEGLU: lambda g, u: u * 0.5 * g * (1 + np.tanh(np.sqrt(2 / np.pi) * g * (1 + 0.044715 * g * g))),
+         O.GLU_REGLU: lambda g, u: u * np.maximum(g, 0)}[glu_op]
+    for tok in range(n_tok):
+        ad = O.dequantize(O.Q8_1, act[tok, 0], K)[0].astype(np.float64)
+        for c in range(n_used):
+            e = ids[tok, c]
+            u = (ud[e] @ ad) * xs[e] + xb[e]
+            g = (gd[e] @ ad) * gs[e] + gb[e]
+            assert np.allclose(dst[tok, c], f(g, u), rtol=2e-5, atol=2e-6)
+        assert np.allclose(sh[tok], f(sgd @ ad, sud @ ad), rtol=2e-5, atol=2e-6)
+
+
+def test_combine_against_numpy():
+    rng = np.random.default_rng(7)
+    o = rng.standard_normal((2, 5, 1024)).astype(np.float32)
+    w = rng.uniform(0, 1, (2, 5)).astype(np.float32)
+    sh = rng.standard_normal((2, 1024)).astype(np.float32)
+    res = rng.standard_normal((2, 1024)).astype(np.float32)
+    x, y = O.combine_q8_1(o, w, shared=sh, residual=res, rms_norm=True, eps=1e-6)
+    want = res.astype(np.float64) + sh + (w[:, :, None].astype(np.float64) * o).sum(1)
+    assert np.allclose(x, want, rtol=1e-6, atol=1e-5)
+    for t in range(2):
+        s = 1.0 / np.sqrt((x[t].astype(np.float64) ** 2).mean() + 1e-6)
+        deq = O.dequantize(O.Q8_1, y[t], 1024)[0]
+        assert O.rel_l2(deq, x[t] * s) < 0.01
+        _, y_plain = O.combine_q8_1(o[t:t + 1], w[t:t + 1], shared=sh[t:t + 1], residual=res[t:t + 1])
+        assert np.array_equal(y_plain[0], O.quantize_q8_1(x[t]))
