@@ -90,7 +90,7 @@ SIGNATURES = [
     ("ggml_hip_quantize_q8_K", C.c_int, [_VP, _VP, _I64, _I64, _I64, _I64, _VP]),
     ("ggml_hip_quantize_q8_0_as_q8_1", C.c_int, [_VP, _VP, _I64, _I64, _I64, _I64, _VP]),
     ("ggml_hip_moe_combine_q8_1", C.c_int,
-     [_VP, _I64, _VP, _I32, _VP, _I64, _VP, _VP, _VP, _I64, _I64, _I64, _I32, C.c_float, _VP]),
+     [_VP, _I64, _VP, _I32, _VP, _I64, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP, C.c_float, _VP]),
     ("ggml_hip_moe_cache_configure", C.c_int, [C.POINTER(Config)]),
     ("ggml_hip_moe_cache_get_config", C.c_int, [C.POINTER(Config)]),
     ("ggml_hip_moe_cache_num_entries", C.c_int, []),
@@ -321,16 +321,18 @@ def stamps_snapshot(i: int, stream=None):
     return out
 
 
-def combine_q8_1(o, w, shared=None, residual=None, x_out=None, y=None, rms_norm=False, eps=1e-6, stream=None):
-    """o: [n_tok, n_used, k] fp32, w: [n_tok, n_used] -> (x_out [n_tok, k], y q8_1 [n_tok, k/32*36])."""
+def combine_q8_1(o, w, shared=None, residual=None, x_out=None, y=None, rms_norm=False, norm_weight=None, eps=1e-6,
+                 stream=None):
+    """o: [n_tok, n_used, k] fp32, w: [n_tok, n_used] -> (x_out [n_tok, k], y q8_1 [n_tok, k/32*36]);
+    with rms_norm, y holds q8_1((x * rms scale) * norm_weight)."""
     torch = _torch()
-    _require_gpu(o, w, shared, residual, x_out, y)
+    _require_gpu(o, w, shared, residual, x_out, y, norm_weight)
     n_tok, n_used, k = o.shape
     if y is None:
         y = torch.empty((n_tok, k // 32 * 36), dtype=torch.uint8, device=o.device)
     check(lib().ggml_hip_moe_combine_q8_1(o.data_ptr(), o.stride(1), w.data_ptr(), n_used, _ptr(shared),
                                           shared.stride(0) if shared is not None else 0, _ptr(residual),
                                           _ptr(x_out), y.data_ptr(), y.stride(0) // 36, k, n_tok,
-                                          1 if rms_norm else 0, eps, _stream(stream)),
+                                          int(bool(rms_norm)), _ptr(norm_weight), eps, _stream(stream)),
           "combine_q8_1")
     return x_out, y

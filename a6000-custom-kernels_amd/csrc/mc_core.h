@@ -1,0 +1,566 @@
+// mc_core.h -- device-side building blocks shared by the per-op GEMV kernels and
+// the persistent decode kernel: fp16/int8 helpers, buffer descriptors, the
+// per-lane activation slice, LDS word readers, the per-type unit dot products,
+// the GLU epilogue and the buffer->LDS span DMA.  Device code only (gfx950).
+#ifndef MC_CORE_H
+#define MC_CORE_H
+
+#include <hip/hip_runtime.h>
+
+#include "mc_internal.h"
+
+namespace mc {
+
+typedef uint32_t u32;
+typedef int32_t i32;
+
+// ---------------------------------------------------------------------------
+// small device helpers
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float h2f(u32 bits16) {
+    return (float) __builtin_bit_cast(_Float16, (uint16_t) (bits16 & 0xFFFFu));
+}
+
+__device__ __forceinline__ uint16_t f2h_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16) f);   // v_cvt_f16_f32, round to nearest even
+}
+
+__device__ __forceinline__ int sdot4(u32 a, u32 b, int c) {
+    return __builtin_amdgcn_sdot4((int) a, (int) b, c, false);
+}
+
+__device__ __forceinline__ u32 byte_of(u32 w, int i) { return (w >> (8 * i)) & 0xFFu; }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, u32 nbytes) {
+    // gfx9 raw buffer: stride 0, num_records in bytes, dword3 = 0x00020000
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short) 0, (int) nbytes, 0x00020000);
+}
+
+__device__ __forceinline__ u32 bload(__amdgpu_buffer_rsrc_t r, u32 off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// activation slice of one lane: UE int8 values, one scale per 32, sums per 16
+// ---------------------------------------------------------------------------
+
+template <int UE>
+struct Act {
+    u32 q[UE / 4];
+    float d[UE / 32];
+    int s16[UE / 16];
+};
+
+template <int UE, int ACT>
+__device__ __forceinline__ void load_act(Act<UE> &A, __amdgpu_buffer_rsrc_t r, u32 row_off, int col) {
+    if constexpr (ACT == ACT_Q8_1) {
+#pragma unroll
+        for (int b = 0; b < UE / 32; ++b) {
+            const u32 off = row_off + (u32) (col * (UE / 32) + b) * 36u;
+            A.d[b] = h2f(bload(r, off));
+#pragma unroll
+            for (int k = 0; k < 8; ++k) A.q[8 * b + k] = bload(r, off + 4u + 4u * k);
+        }
+    } else {
+        static_assert(UE == 256, "q8_K activations pair with 256-value units");
+        const u32 off = row_off + (u32) col * 292u;
+        const float d = __builtin_bit_cast(float, bload(r, off));
+#pragma unroll
+        for (int b = 0; b < 8; ++b) A.d[b] = d;
+#pragma unroll
+        for (int k = 0; k < 64; ++k) A.q[k] = bload(r, off + 4u + 4u * k);
+    }
+#pragma unroll
+    for (int s = 0; s < UE / 16; ++s) {
+        int t = sdot4(A.q[4 * s + 0], 0x01010101u, 0);
+        t = sdot4(A.q[4 * s + 1], 0x01010101u, t);
+        t = sdot4(A.q[4 * s + 2], 0x01010101u, t);
+        A.s16[s] = sdot4(A.q[4 * s + 3], 0x01010101u, t);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// LDS word readers for one unit
+// ---------------------------------------------------------------------------
+
+struct WordsAligned {            // unit starts on a 4-byte boundary
+    const u32 *p;
+    __device__ __forceinline__ u32 operator[](int i) const { return p[i]; }
+};
+
+struct WordsShifted {            // unit starts on a 2-byte boundary: realign with v_alignbyte
+    const u32 *p;
+    u32 sh;                      // byte shift 0..3
+    __device__ __forceinline__ u32 operator[](int i) const { return __builtin_amdgcn_alignbyte(p[i + 1], p[i], sh); }
+};
+
+// ---------------------------------------------------------------------------
+// per-type unit dot products
+// ---------------------------------------------------------------------------
+
+// Q2_K: scales[16] | qs[64] | d | dmin.  Element i = 128h + 32j + l uses
+// (qs[32h + l] >> 2j) & 3 and sub-block scale byte i >> 4 (lo 4: scale, hi 4: min).
+template <int ACT, class W>
+__device__ __forceinline__ float dot_q2_K(const W &w, const Act<256> &A) {
+    const u32 dm = w[20];
+    const float d = h2f(dm), dmin = h2f(dm >> 16);
+    u32 sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[i] = w[i];
+    float accI = 0.0f, accM = 0.0f;
+    int isum = 0, msum = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        u32 q[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) q[k] = w[4 + 8 * h + k];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int g = 4 * h + j;
+            // j < 3: keep the 2-bit field in place (value * 4^j); j == 3: shift down
+            const int jj = j < 3 ? j : 0;
+            int d0 = 0, d1 = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const u32 v0 = j < 3 ? (q[k] & (0x03030303u << (2 * j))) : ((q[k] >> 6) & 0x03030303u);
+                const u32 v1 = j < 3 ? (q[k + 4] & (0x03030303u << (2 * j))) : ((q[k + 4] >> 6) & 0x03030303u);
+                d0 = sdot4(v0, A.q[8 * g + k], d0);
+                d1 = sdot4(v1, A.q[8 * g + 4 + k], d1);
+            }
+            const u32 b0 = byte_of(sc[(2 * g) >> 2], (2 * g) & 3);
+            const u32 b1 = byte_of(sc[(2 * g + 1) >> 2], (2 * g + 1) & 3);
+            const int is = (int) (b0 & 0xF) * d0 + (int) (b1 & 0xF) * d1;
+            const int ms = (int) (b0 >> 4) * A.s16[2 * g] + (int) (b1 >> 4) * A.s16[2 * g + 1];
+            if constexpr (ACT == ACT_Q8_K) {
+                isum += is >> (2 * jj);
+                msum += ms;
+            } else {
+                const float fi = (float) is * (jj == 0 ? 1.0f : (jj == 1 ? 0.25f : 0.0625f));
+                accI = fmaf(A.d[g], fi, accI);
+                accM = fmaf(A.d[g], (float) ms, accM);
+            }
+        }
+    }
+    if constexpr (ACT == ACT_Q8_K) {
+#pragma clang fp contract(off)
+        const float dall = A.d[0] * d, dmn = A.d[0] * dmin;
+        return dall * (float) isum - dmn * (float) msum;
+    } else {
+        return d * accI - dmin * accM;
+    }
+}
+
+// Q3_K: hmask[32] | qs[64] | scales[12] | d.  Element i = 128h + 32j + l:
+// low2 = (qs[32h + l] >> 2j) & 3, hbit = hmask[l] bit (4h + j), code = low2 + 4*hbit - 4;
+// 6-bit scale of sub-block s: low 4 from byte s (s < 8) or byte s-8 >> 4, high 2 from
+// byte 8 + (s & 3) bits 2*(s >> 2); value - 32.
+template <int ACT, class W>
+__device__ __forceinline__ float dot_q3_K(const W &w, const Act<256> &A) {
+    const float d = h2f(w[27]);
+    const u32 A0 = w[24], A1 = w[25], A2 = w[26];
+    u32 S[4];
+    S[0] = (A0 & 0x0F0F0F0Fu) | ((A2 & 0x03030303u) << 4);
+    S[1] = (A1 & 0x0F0F0F0Fu) | (((A2 >> 2) & 0x03030303u) << 4);
+    S[2] = ((A0 >> 4) & 0x0F0F0F0Fu) | (((A2 >> 4) & 0x03030303u) << 4);
+    S[3] = ((A1 >> 4) & 0x0F0F0F0Fu) | (((A2 >> 6) & 0x03030303u) << 4);
+    u32 hm[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) hm[k] = w[k];
+    float acc = 0.0f;
+    int isum = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        u32 q[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) q[k] = w[8 + 8 * h + k];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int g = 4 * h + j;
+            int d0 = 0, d1 = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const u32 u0 = ((q[k] >> (2 * j)) & 0x03030303u) | (((hm[k] >> (4 * h + j)) & 0x01010101u) << 2);
+                const u32 u1 = ((q[k + 4] >> (2 * j)) & 0x03030303u) | (((hm[k + 4] >> (4 * h + j)) & 0x01010101u) << 2);
+                d0 = sdot4(u0, A.q[8 * g + k], d0);
+                d1 = sdot4(u1, A.q[8 * g + 4 + k], d1);
+            }
+            d0 -= 4 * A.s16[2 * g];
+            d1 -= 4 * A.s16[2 * g + 1];
+            const int s0 = 2 * g, s1 = 2 * g + 1;
+            const int sc0 = (int) byte_of(S[s0 >> 2], s0 & 3) - 32;
+            const int sc1 = (int) byte_of(S[s1 >> 2], s1 & 3) - 32;
+            const int is = sc0 * d0 + sc1 * d1;
+            if constexpr (ACT == ACT_Q8_K) isum += is;
+            else acc = fmaf(A.d[g], (float) is, acc);
+        }
+    }
+    if constexpr (ACT == ACT_Q8_K) {
+#pragma clang fp contract(off)
+        const float dall = A.d[0] * d;
+        return dall * (float) isum;
+    } else {
+        return d * acc;
+    }
+}
+
+// 6-bit scales/mins of Q4_K / Q5_K from the 12 scale bytes (three words S0..S2):
+// sub-block j < 4: sc = b[j] & 63, m = b[j+4] & 63;
+// j >= 4: sc = (b[j+4] & 15) | (b[j-4] >> 6) << 4, m = (b[j+4] >> 4) | (b[j] >> 6) << 4.
+__device__ __forceinline__ void kq_scales(u32 S0, u32 S1, u32 S2, u32 &SC0, u32 &SC1, u32 &M0, u32 &M1) {
+    SC0 = S0 & 0x3F3F3F3Fu;
+    M0 = S1 & 0x3F3F3F3Fu;
+    SC1 = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
+    M1 = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
+}
+
+// Q4_K: d | dmin | scales[12] | qs[128].  Chunk c = i / 64: low nibbles of
+// qs[32c..32c+31] are sub-block 2c, high nibbles sub-block 2c+1.
+// Q5_K: d | dmin | scales[12] | qh[32] | qs[128]; high bit of element l of
+// sub-block g is qh[l] bit g.
+template <int ACT, bool Q5, class W>
+__device__ __forceinline__ float dot_q45_K(const W &w, const Act<256> &A) {
+    const u32 dm = w[0];
+    const float d = h2f(dm), dmin = h2f(dm >> 16);
+    u32 SC0, SC1, M0, M1;
+    kq_scales(w[1], w[2], w[3], SC0, SC1, M0, M1);
+    constexpr int QS = Q5 ? 12 : 4;
+    float accI = 0.0f, accM = 0.0f;
+    int isum = 0, msum = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        u32 q[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) q[k] = w[QS + 8 * c + k];
+#pragma unroll
+        for (int hi = 0; hi < 2; ++hi) {
+            const int g = 2 * c + hi;
+            int dot = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                u32 v = hi ? ((q[k] >> 4) & 0x0F0F0F0Fu) : (q[k] & 0x0F0F0F0Fu);
+                if constexpr (Q5) v |= ((w[4 + k] >> g) & 0x01010101u) << 4;
+                dot = sdot4(v, A.q[8 * g + k], dot);
+            }
+            const int sc = (int) byte_of(g < 4 ? SC0 : SC1, g & 3);
+            const int m = (int) byte_of(g < 4 ? M0 : M1, g & 3);
+            const int is = sc * dot;
+            const int ms = m * (A.s16[2 * g] + A.s16[2 * g + 1]);
+            if constexpr (ACT == ACT_Q8_K) {
+                isum += is;
+                msum += ms;
+            } else {
+                accI = fmaf(A.d[g], (float) is, accI);
+                accM = fmaf(A.d[g], (float) ms, accM);
+            }
+        }
+    }
+    if constexpr (ACT == ACT_Q8_K) {
+#pragma clang fp contract(off)
+        const float dall = A.d[0] * d, dmn = A.d[0] * dmin;
+        return dall * (float) isum - dmn * (float) msum;
+    } else {
+        return d * accI - dmin * accM;
+    }
+}
+
+// Q6_K: ql[128] | qh[64] | scales[16] (int8) | d.  Element i = 128n + 32q + l:
+// low 4 = ql[64n + 32(q & 1) + l] (q >= 2: high nibble), high 2 = (qh[32n + l] >> 2q) & 3,
+// code - 32; scale byte i >> 4.
+template <int ACT, class W>
+__device__ __forceinline__ float dot_q6_K(const W &w, const Act<256> &A) {
+    const float d = h2f(w[52]);
+    u32 sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[i] = w[48 + i];
+    float acc = 0.0f;
+    int isum = 0;
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+        u32 qh[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) qh[k] = w[32 + 8 * n + k];
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+            const int g = 4 * n + qq;
+            int d0 = 0, d1 = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const u32 ql = w[16 * n + 8 * (qq & 1) + k];
+                const u32 v = ((qq >> 1) ? ((ql >> 4) & 0x0F0F0F0Fu) : (ql & 0x0F0F0F0Fu)) |
+                              (((qh[k] >> (2 * qq)) & 0x03030303u) << 4);
+                if (k < 4) d0 = sdot4(v, A.q[8 * g + k], d0);
+                else       d1 = sdot4(v, A.q[8 * g + k], d1);
+            }
+            d0 -= 32 * A.s16[2 * g];
+            d1 -= 32 * A.s16[2 * g + 1];
+            const int s0 = 2 * g, s1 = 2 * g + 1;
+            const int sc0 = (int) (int8_t) byte_of(sc[s0 >> 2], s0 & 3);
+            const int sc1 = (int) (int8_t) byte_of(sc[s1 >> 2], s1 & 3);
+            const int is = sc0 * d0 + sc1 * d1;
+            if constexpr (ACT == ACT_Q8_K) isum += is;
+            else acc = fmaf(A.d[g], (float) is, acc);
+        }
+    }
+    if constexpr (ACT == ACT_Q8_K) {
+#pragma clang fp contract(off)
+        const float dall = A.d[0] * d;
+        return dall * (float) isum;
+    } else {
+        return d * acc;
+    }
+}
+
+// spread the low 4 bits of x to bit 0 of the 4 bytes
+__device__ __forceinline__ u32 spread4(u32 x) { return ((x & 0xFu) * 0x00204081u) & 0x01010101u; }
+
+// Legacy units: two 32-value blocks.  Q4_0 = d | qs[16] (low nibble: j, high: j+16),
+// offset 8.  Q5_0 = d | qh[4] | qs[16] (5th bit of value j is qh bit j), offset 16.
+// Q8_0 = d | int8 qs[32].
+template <int T, class W>
+__device__ __forceinline__ float dot_legacy(const W &w, const Act<64> &A) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        int sumi = 0;
+        float dw;
+        if constexpr (T == T_Q4_0) {
+            // block 0 at byte 0 (qs at 2: realign), block 1 at byte 18 (qs at 20)
+            dw = b == 0 ? h2f(w[0]) : h2f(w[4] >> 16);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const u32 q = b == 0 ? __builtin_amdgcn_alignbyte(w[k + 1], w[k], 2) : w[5 + k];
+                sumi = sdot4(q & 0x0F0F0F0Fu, A.q[8 * b + k], sumi);
+                sumi = sdot4((q >> 4) & 0x0F0F0F0Fu, A.q[8 * b + 4 + k], sumi);
+            }
+            sumi -= 8 * (A.s16[2 * b] + A.s16[2 * b + 1]);
+        } else if constexpr (T == T_Q5_0) {
+            // block 0 at byte 0 (qh at 2, qs at 6), block 1 at byte 22 (qh at 24, qs at 28)
+            dw = b == 0 ? h2f(w[0]) : h2f(w[5] >> 16);
+            const u32 qh = b == 0 ? __builtin_amdgcn_alignbyte(w[1], w[0], 2) : w[6];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const u32 q = b == 0 ? __builtin_amdgcn_alignbyte(w[k + 2], w[k + 1], 2) : w[7 + k];
+                const u32 lo = (q & 0x0F0F0F0Fu) | (spread4(qh >> (4 * k)) << 4);
+                const u32 hi = ((q >> 4) & 0x0F0F0F0Fu) | (spread4(qh >> (16 + 4 * k)) << 4);
+                sumi = sdot4(lo, A.q[8 * b + k], sumi);
+                sumi = sdot4(hi, A.q[8 * b + 4 + k], sumi);
+            }
+            sumi -= 16 * (A.s16[2 * b] + A.s16[2 * b + 1]);
+        } else {
+            // block 0 at byte 0 (qs at 2), block 1 at byte 34 (qs at 36)
+            dw = b == 0 ? h2f(w[0]) : h2f(w[8] >> 16);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const u32 q = b == 0 ? __builtin_amdgcn_alignbyte(w[k + 1], w[k], 2) : w[9 + k];
+                sumi = sdot4(q, A.q[8 * b + k], sumi);
+            }
+        }
+        acc += (float) sumi * dw * A.d[b];
+    }
+    return acc;
+}
+
+template <int T, int ACT, class W>
+__device__ __forceinline__ float unit_dot(const W &w, const Act<type_geom(T).unit_elems> &A) {
+    if constexpr (T == T_Q2_K) return dot_q2_K<ACT>(w, A);
+    else if constexpr (T == T_Q3_K) return dot_q3_K<ACT>(w, A);
+    else if constexpr (T == T_Q4_K) return dot_q45_K<ACT, false>(w, A);
+    else if constexpr (T == T_Q5_K) return dot_q45_K<ACT, true>(w, A);
+    else if constexpr (T == T_Q6_K) return dot_q6_K<ACT>(w, A);
+    else return dot_legacy<T>(w, A);
+}
+
+// ---------------------------------------------------------------------------
+// GLU (kernels/moe-cache.cu:264-280; ggml unary definitions)
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float glu_apply(int op, float g, float up, float limit) {
+    switch (op) {
+        case 0: return up * (g > 0.0f ? g : 0.0f);                                                   // REGLU
+        case 1: return up * (0.5f * g * (1.0f + tanhf(0.79788456080286535587989211986876f * g * (1.0f + 0.044715f * g * g)))); // GEGLU
+        case 2: return up * silu_f(g);                                                               // SWIGLU
+        case 3: {                                                                                    // SWIGLU_OAI
+            const float x = fminf(g, 7.0f);
+            const float u = fmaxf(fminf(up, 7.0f), -7.0f);
+            return x / (1.0f + expf(-x * 1.702f)) * (1.0f + u);
+        }
+        case 4: return up * (0.5f * g * (1.0f + erff(g * 0.70710678118654752440f)));               // GEGLU_ERF
+        case 5: return up * (g / (1.0f + expf(-1.702f * g)));                                       // GEGLU_QUICK
+        case 6: {                                                                                    // SWIGLU_CLAMP
+            const float x = fminf(g, limit);
+            const float u = fmaxf(fminf(up, limit), -limit);
+            return silu_f(x) * u;
+        }
+        default: return up * g;
+    }
+}
+
+
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <int T>
+__device__ __forceinline__ void dma_span(const uint8_t *base, u32 base_bytes, u32 start, u32 nbytes, uint8_t *lds) {
+    // stream [start, start + nbytes) of the matrix at `base` into lds: lds[x] = byte (start & ~15) + x
+    const uintptr_t abase = (uintptr_t) base & ~(uintptr_t) 15;
+    const u32 skew = (u32) ((uintptr_t) base - abase);
+    const __amdgpu_buffer_rsrc_t r = make_rsrc((const void *) abase, base_bytes + skew);
+    const u32 a0 = (start + skew) & ~15u;
+    const u32 lead = (start + skew) - a0;
+    const int rounds = (int) ((lead + nbytes + 1023u) >> 10);
+    constexpr int MAXR = span_lds_bytes(T) / 1024;
+    const u32 lane_off = a0 + 16u * threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < MAXR; ++i) {
+        if (i < rounds) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * i), 16, lane_off + 1024u * i, 0, 0, 0);
+        }
+    }
+}
+
+// Byte offset, inside the LDS copy made by dma_span, of byte `start` of the matrix at `base`.
+__device__ __forceinline__ u32 span_lead(const uint8_t *base, u32 start) {
+    const uintptr_t abase = (uintptr_t) base & ~(uintptr_t) 15;
+    return (u32) ((start + ((uintptr_t) base - abase)) & 15u);
+}
+
+// Dot of the lane's unit `unit` of a DMA'd span (lead from span_lead) with its activation slice.
+template <int T, int ACT>
+__device__ __forceinline__ float span_unit_dot(const uint8_t *lds_span, u32 lead, int unit,
+                                               const Act<type_geom(T).unit_elems> &A) {
+    constexpr TypeGeom G = type_geom(T);
+    const u32 uoff = lead + (u32) unit * G.unit_bytes;
+    if constexpr (G.aligned) {
+        return unit_dot<T, ACT>(WordsAligned{(const u32 *) (lds_span + uoff)}, A);
+    } else {
+        return unit_dot<T, ACT>(WordsShifted{(const u32 *) (lds_span + (uoff & ~3u)), uoff & 3u}, A);
+    }
+}
+
+// Makes a wave's LDS writes visible to the wave's later LDS reads (single-wave workgroups).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Row sums of a step in a fixed order: lane r*nu adds the nu lane partials of row r left to right.
+// red: 64 floats of LDS.  The sum is valid in lanes with (lane % nu) == 0.
+__device__ __forceinline__ float step_row_sum(float *red, float v, int nu) {
+    const int lane = threadIdx.x % WAVE;
+    red[lane] = v;
+    wave_lds_sync();
+    float s = 0.0f;
+    if (lane % nu == 0 && lane + nu <= WAVE)
+        for (int i = 0; i < nu; ++i) s += red[lane + i];
+    wave_lds_sync();
+    return s;
+}
+
+// q8_1 quantization of one 32-value block spread over a 32-lane half-wave (the
+// arithmetic of ggml-CUDA quantize_q8_1): amax over the half-wave, d = amax/127
+// (IEEE division), q = amax == 0 ? 0 : roundf(x/d).  Also returns the xor-butterfly sum.
+__device__ __forceinline__ int8_t q8_1_lane(float x, float &d, float &sum) {
+    float amax = fabsf(x);
+    sum = x;
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+        sum += __shfl_xor(sum, off, 32);
+    }
+    d = amax / 127.0f;
+    return amax == 0.0f ? (int8_t) 0 : (int8_t) roundf(x / d);
+}
+
+constexpr int COMBINE_MAX_USED = 16;
+
+// One 64-lane wave: the 256 combined values of chunk j of a row
+//   x = residual + shared + sum_c w[c] * o[c]   (c ascending, fmaf)
+// into xs (row-relative index) and x_out (when given); returns the chunk's RMS
+// sum in the canonical order (mc_internal.h) in every lane.
+__device__ __forceinline__ float combine_chunk(const float *o, int64_t o_stride, const float *w, int n_used,
+                                               const float *shared, const float *residual, float *x_out, float *xs,
+                                               int j) {
+    const int lane = threadIdx.x % WAVE;
+    float wc[COMBINE_MAX_USED];
+#pragma unroll
+    for (int c = 0; c < COMBINE_MAX_USED; ++c) wc[c] = c < n_used ? w[c] : 0.0f;
+    float a = 0.0f;
+#pragma unroll
+    for (int p = 0; p < RMS_CHUNK / WAVE; ++p) {
+        const int64_t i = (int64_t) j * RMS_CHUNK + WAVE * p + lane;
+        float ov[COMBINE_MAX_USED];
+#pragma unroll
+        for (int c = 0; c < COMBINE_MAX_USED; ++c) ov[c] = c < n_used ? o[c * o_stride + i] : 0.0f;
+        float x = residual ? residual[i] : 0.0f;
+        if (shared) x += shared[i];
+#pragma unroll
+        for (int c = 0; c < COMBINE_MAX_USED; ++c)
+            if (c < n_used) x = fmaf(wc[c], ov[c], x);
+        if (x_out) x_out[i] = x;
+        xs[i] = x;
+        a = fmaf(x, x, a);
+    }
+#pragma unroll
+    for (int off = WAVE / 2; off > 0; off >>= 1) {
+        const float other = __shfl_down(a, off, WAVE);
+        if (lane < off) a += other;
+    }
+    return __shfl(a, 0, WAVE);
+}
+
+// One 64-lane wave: q8_1 of the 256 values v of chunk j into y (row base), with
+// v = (xs[i] * s) * nw[i] under norm (nw optional) and v = xs[i] otherwise.
+__device__ __forceinline__ void quantize_chunk(const float *xs, bool norm, float s, const float *nw, uint8_t *y,
+                                               int j) {
+    const int lane = threadIdx.x % WAVE;
+#pragma unroll
+    for (int p = 0; p < RMS_CHUNK / WAVE; ++p) {
+        const int i = j * RMS_CHUNK + WAVE * p + lane;
+        float v = xs[i];
+        if (norm) {
+            v *= s;
+            if (nw) v *= nw[i];
+        }
+        float d, sum;
+        const int8_t q = q8_1_lane(v, d, sum);
+        uint8_t *yb = y + (i / 32) * 36;
+        yb[4 + (lane & 31)] = (uint8_t) q;
+        if ((lane & 31) == 0) *(u32 *) yb = (u32) f2h_bits(d) | ((u32) f2h_bits(sum) << 16);
+    }
+}
+
+// q8_1 codes and scales of a row of k fp32 values (k % 64 == 0) into LDS with the
+// arithmetic of the q8_1 quantizer: codes[i] int8, dsc[b] = the block's fp16 scale as float.
+__device__ __forceinline__ void quantize_row_to_lds(const float *x, int k, int8_t *codes, float *dsc) {
+    const int lane = threadIdx.x % WAVE;
+    for (int base = 0; base < k; base += WAVE) {
+        float d, sum;
+        const int8_t q = q8_1_lane(x[base + lane], d, sum);
+        codes[base + lane] = q;
+        if ((lane & 31) == 0) dsc[(base + lane) / 32] = h2f(f2h_bits(d));
+    }
+}
+
+// The lane's 256-value activation slice `col` from quantize_row_to_lds output.
+__device__ __forceinline__ void load_act_lds(Act<256> &A, const int8_t *codes, const float *dsc, int col) {
+    const u32 *cw = (const u32 *) (codes + col * 256);
+#pragma unroll
+    for (int k = 0; k < 64; ++k) A.q[k] = cw[k];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) A.d[b] = dsc[col * 8 + b];
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        int t = sdot4(A.q[4 * s + 0], 0x01010101u, 0);
+        t = sdot4(A.q[4 * s + 1], 0x01010101u, t);
+        t = sdot4(A.q[4 * s + 2], 0x01010101u, t);
+        A.s16[s] = sdot4(A.q[4 * s + 3], 0x01010101u, t);
+    }
+}
+
+}  // namespace mc
+
+#endif

@@ -747,9 +747,10 @@ int ggml_hip_quantize_q8_0_as_q8_1(const float *x, void *y, int64_t k, int64_t n
 
 int ggml_hip_moe_combine_q8_1(const float *o, int64_t o_stride, const float *w, int32_t n_used, const float *shared,
                               int64_t shared_stride, const float *residual, float *x_out, void *y_q8_1, int64_t y_stride,
-                              int64_t k, int64_t n_tok, int32_t rms_norm, float eps, void *stream) {
+                              int64_t k, int64_t n_tok, int32_t rms_norm, const float *norm_weight, float eps,
+                              void *stream) {
     if (!y_q8_1 || (n_used > 0 && (!o || !w))) return fail(E_INVALID, "combine: null argument");
-    if (k <= 0 || k % 32 || k > 8192 || n_used < 0 || n_used > 16 || n_tok < 0 || (n_used > 0 && o_stride < k) ||
+    if (k <= 0 || k % 256 || k > 8192 || n_used < 0 || n_used > 16 || n_tok < 0 || (n_used > 0 && o_stride < k) ||
         (shared && shared_stride < k) || y_stride < k / 32)
         return fail(E_INVALID, "combine: bad shape");
     if ((uintptr_t) y_q8_1 & 3u) return fail(E_INVALID, "combine: misaligned output");
@@ -766,7 +767,8 @@ int ggml_hip_moe_combine_q8_1(const float *o, int64_t o_stride, const float *w, 
     c.k = k;
     c.n_used = n_used;
     c.n_tok = (int32_t) n_tok;
-    c.rms_norm = rms_norm ? 1 : 0;
+    c.rms_norm = rms_norm != 0;
+    c.norm_weight = norm_weight;
     c.eps = eps;
     const int rc = dev()->launch_combine(c, stream);
     if (rc) return dev_err(rc, "combine launch");

@@ -138,9 +138,18 @@ struct CombineArgs {
     int64_t k;
     int32_t n_used;
     int32_t n_tok;
-    int32_t rms_norm;        // 1: quantize x / rms(x) (weightless RMSNorm), 0: quantize x
+    int32_t rms_norm;        // quantize (x * rms scale) * norm_weight instead of x
+    const float *norm_weight;  // [k] or null
     float eps;
 };
+
+// Canonical order of the RMS sum of a row of k values (k % 256 == 0), shared by
+// the combine kernel, the persistent decode kernel and the CPU oracle: chunk j
+// holds values [256j, 256j+256); lane l of a 64-lane group accumulates
+// v = x[256j + 64p + l] for p = 0..3 as a = fmaf(v, v, a) starting from 0;
+// the 64 lane sums are tree-added (lane l += lane l+off, off = 32, 16, ..., 1);
+// chunk sums are added in ascending j starting from 0; s = 1 / sqrtf(sum/k + eps).
+constexpr int RMS_CHUNK = 256;
 
 }  // namespace mc
 

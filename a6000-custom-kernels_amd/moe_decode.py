@@ -2,12 +2,13 @@
 
 Per layer, for one token (the op sequence of a ggml MoE FFN block):
   1. gate/up MUL_MAT_ID over the routed experts, fused SwiGLU, with the shared
-     expert's gate/up in the same launch          -> h[0..n_used)   and h[n_used]
+     expert's gate/up in the same launch             -> h[0..n_used)   and h[n_used]
   2. q8_1 quantization of the n_used+1 GLU rows    -> hq
   3. down MUL_MAT_ID (one activation row per slot), shared expert's down in the
      same launch                                    -> o[0..n_used) and o_sh
-  4. combine x' = x + o_sh + sum_j w_j o_j, fused with the q8_1 quantization of
-     x' for the next layer's gate/up launch.
+  4. combine x' = x + o_sh + sum_j w_j o_j, fused with the next block's
+     ffn_norm (RMSNorm times its norm weight) and the q8_1 quantization of the
+     normalized row for the next layer's gate/up launch.
 Every launch goes through the C ABI (include/ggml_hip_moe_cache.h); one token is
 captured once into a hipGraph and replayed, with routing ids and router
 weights copied into fixed device buffers before each replay.
@@ -91,6 +92,8 @@ class MoeDecodeModel:
         self.o_sh = torch.zeros((1, hidden), dtype=f32, device=device)
         self.ids = torch.zeros((n_layers, 1, n_used), dtype=i32, device=device)
         self.w = torch.zeros((n_layers, 1, n_used), dtype=f32, device=device)
+        # ffn_norm weight of each layer (RMSNorm in front of its MoE block)
+        self.norm = torch.empty((n_layers, hidden), dtype=f32, device=device).uniform_(0.5, 1.5, generator=gen)
         for ly in self.layers:
             ly.f_gu = make_fusion(gate=ly.gate, glu_op=GLU_SWIGLU, shared_up=ly.sh_up, shared_gate=ly.sh_gate,
                                   shared_dst=self.h[n_used:], shared_type=sh_type)
@@ -106,7 +109,8 @@ class MoeDecodeModel:
         sh = row_bytes(self.sh_type, H) * F * 2 + row_bytes(self.sh_type, F) * H
         act = H // 32 * 36 + (U + 1) * F // 32 * 36
         out = (U + 1) * F * 4 + (U + 1) * H * 4
-        return self.L * (U * (2 * eb_gu + eb_dn) + sh + act + out)
+        norm = H * 4
+        return self.L * (U * (2 * eb_gu + eb_dn) + sh + act + out + norm)
 
     def gate_up_bytes(self):
         H, F, U = self.H, self.F, self.U
@@ -144,16 +148,19 @@ class MoeDecodeModel:
         check(lib().ggml_hip_quantize_q8_1(self.h.data_ptr(), self.hq.data_ptr(), F, U + 1, F, F // 32, s), "quantize h")
         self.launch_down(l, s)
         src, dst = (self.x, self.x_next) if l % 2 == 0 else (self.x_next, self.x)
+        nxt = self.norm[(l + 1) % self.L]        # the next block's ffn_norm (layer 0's for the next token)
         check(lib().ggml_hip_moe_combine_q8_1(self.o.data_ptr(), H, self.w[l].data_ptr(), U, self.o_sh.data_ptr(), H,
                                               src.data_ptr() if self.residual else None, dst.data_ptr(),
-                                              self.y.data_ptr(), H // 32, H, 1, 1, self.eps, s), "combine")
+                                              self.y.data_ptr(), H // 32, H, 1, 1, nxt.data_ptr(), self.eps, s),
+              "combine")
 
     def launch_token(self):
         """One token through every layer; the token's input and output are in self.x."""
         s = self._stream()
-        # RMS-normalized q8_1 of the input (the ffn_norm in front of the first MoE block)
+        # ffn_norm of the first MoE block and q8_1 of its output
         check(lib().ggml_hip_moe_combine_q8_1(None, 0, None, 0, None, 0, self.x.data_ptr(), None, self.y.data_ptr(),
-                                              self.H // 32, self.H, 1, 1, self.eps, s), "quantize x")
+                                              self.H // 32, self.H, 1, 1, self.norm[0].data_ptr(), self.eps, s),
+              "norm x")
         for l in range(self.L):
             self.launch_layer(l, s)
         if self.L % 2 == 1:

@@ -196,17 +196,20 @@ int ggml_hip_quantize_q8_0_as_q8_1(const float *x, void *y, int64_t k, int64_t n
 
 /* The MoE output combine that follows MUL_MAT_ID in a ggml graph (MUL by the
  * router weights, ADD of the shared expert and of the residual), fused with the
- * (optionally RMS-normalized) q8_1 quantization of the result for the next GEMV:
+ * RMSNorm (RMS_NORM, then MUL by the norm weight) in front of the next MoE block
+ * and the q8_1 quantization of its result for the next GEMV:
  *   x[t] = residual[t] + shared[t] + sum_{j < n_used} w[t][j] * o[t][j]   (j ascending, fused multiply-add)
- *   y[t] = q8_1(x[t] * s), s = rms_norm ? 1/sqrt(mean(x[t]^2) + eps) : 1
- * o: [n_tok][n_used][o_stride] floats; w: [n_tok][n_used]; shared: [n_tok][shared_stride] or NULL;
- * residual: [n_tok][k] or NULL; x_out: [n_tok][k] or NULL; y_q8_1: n_tok rows, y_stride blocks apart;
- * k <= 8192.  No reference counterpart (ggml runs these as separate ops); q8_1 semantics as
- * ggml_hip_quantize_q8_1; the mean of squares is summed in a fixed order (deterministic). */
+ *   v[t] = rms_norm ? (x[t] * (1/sqrt(mean(x[t]^2) + eps))) * norm_weight : x[t]   (norm_weight optional)
+ *   y[t] = q8_1(v[t])
+ * The mean of squares is summed in a fixed order (256-value chunks, see mc_internal.h), so results are
+ * deterministic.  o: [n_tok][n_used][o_stride] floats (n_used <= 16); w: [n_tok][n_used]; shared:
+ * [n_tok][shared_stride] or NULL; residual: [n_tok][k] or NULL; x_out: [n_tok][k] or NULL; y_q8_1: n_tok
+ * rows, y_stride blocks apart; norm_weight: [k] or NULL; k % 256 == 0, k <= 8192.  No reference
+ * counterpart (ggml runs these as separate ops). */
 int ggml_hip_moe_combine_q8_1(const float *o, int64_t o_stride, const float *w, int32_t n_used,
                               const float *shared, int64_t shared_stride, const float *residual,
                               float *x_out, void *y_q8_1, int64_t y_stride, int64_t k, int64_t n_tok,
-                              int32_t rms_norm, float eps, void *stream);
+                              int32_t rms_norm, const float *norm_weight, float eps, void *stream);
 
 /* ---------------------------------------------------------------------
  * Configuration, introspection and teardown (the reference reads env vars

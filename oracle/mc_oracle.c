@@ -840,7 +840,7 @@ int or_mul_mat_id(const or_mmid_args *A) {
             float up = or_vec_dot(A->sh_type, A->act_kind, K, (const char *) A->sh_up + r * srb, arow);
             float out = up;
             if (A->sh_gate) {
-                const float g = or_vec_dot(A->sh_type, A->act_kind, K, (const char *) A->sh_gate + r * srb, arow);
+                float g = or_vec_dot(A->sh_type, A->act_kind, K, (const char *) A->sh_gate + r * srb, arow);
                 out = or_glu(A->glu_op, g, up, A->glu_limit);
             }
             A->sh_dst[(int64_t) t * A->sh_stride_col_dst + r] = out;
@@ -916,36 +916,51 @@ int or_cpu_mul_mat_id_f32(int type, int64_t ne00, int64_t ne01, int32_t n_as,
     return 0;
 }
 
-/* The combine is written the way the GPU kernel's 1024 threads split the row so
- * that the normalization is reproduced bit for bit: thread t owns elements
- * t, t+1024, ...; its partial sum of squares accumulates with fmaf in that
- * order; the 1024 partials are tree-summed with offsets 512, 256, ..., 1. */
-#define OR_COMBINE_THREADS 1024
+/* RMS sum of a row in the canonical order of the GPU kernels: 256-value chunks;
+ * in chunk j, partial l (0..63) accumulates x[256j + 64p + l]^2 (p = 0..3) with
+ * fmaf from 0; the 64 partials are tree-added (l += l + off, off = 32 .. 1);
+ * chunk sums are added in ascending j from 0. */
+float or_rms_sum(const float *x, int64_t k) {
+    float total = 0.0f;
+    for (int64_t j = 0; j < k / 256; ++j) {
+        float part[64];
+        for (int l = 0; l < 64; ++l) {
+            float a = 0.0f;
+            for (int p = 0; p < 4; ++p) {
+                const float v = x[256 * j + 64 * p + l];
+                a = fmaf(v, v, a);
+            }
+            part[l] = a;
+        }
+        for (int off = 32; off > 0; off >>= 1)
+            for (int l = 0; l < off; ++l) part[l] += part[l + off];
+        total += part[0];
+    }
+    return total;
+}
+
 void or_combine_q8_1(const float *o, int64_t o_stride, const float *w, int32_t n_used, const float *shared,
                      int64_t shared_stride, const float *residual, float *x_out, void *y, int64_t k, int64_t n_tok,
-                     int32_t rms_norm, float eps) {
-    float *xs = (float *) malloc(sizeof(float) * (size_t) k);
+                     int32_t rms_norm, const float *norm_weight, float eps) {
+    float *v = (float *) malloc(sizeof(float) * (size_t) k);
     for (int64_t t = 0; t < n_tok; ++t) {
-        float part[OR_COMBINE_THREADS];
-        for (int th = 0; th < OR_COMBINE_THREADS; ++th) part[th] = 0.0f;
+        float *x = x_out + t * k;
         for (int64_t i = 0; i < k; ++i) {
-            float v = residual ? residual[t * k + i] : 0.0f;
-            if (shared) v += shared[t * shared_stride + i];
-            for (int32_t j = 0; j < n_used; ++j) v = fmaf(w[t * n_used + j], o[(t * n_used + j) * o_stride + i], v);
-            if (x_out) x_out[t * k + i] = v;
-            part[i % OR_COMBINE_THREADS] = fmaf(v, v, part[i % OR_COMBINE_THREADS]);
-            xs[i] = v;
+            float a = residual ? residual[t * k + i] : 0.0f;
+            if (shared) a += shared[t * shared_stride + i];
+            for (int32_t j = 0; j < n_used; ++j) a = fmaf(w[t * n_used + j], o[(t * n_used + j) * o_stride + i], a);
+            x[i] = a;
         }
-        float scale = 1.0f;
-        if (rms_norm) {
-            for (int off = OR_COMBINE_THREADS / 2; off > 0; off >>= 1)
-                for (int th = 0; th < off; ++th) part[th] += part[th + off];
-            scale = 1.0f / sqrtf(part[0] / (float) k + eps);
+        const float s = rms_norm ? 1.0f / sqrtf(or_rms_sum(x, k) / (float) k + eps) : 1.0f;
+        for (int64_t i = 0; i < k; ++i) {
+            float a = x[i];
+            if (rms_norm) a *= s;
+            if (rms_norm && norm_weight) a *= norm_weight[i];
+            v[i] = a;
         }
-        for (int64_t i = 0; i < k; ++i) xs[i] = xs[i] * scale;
-        or_quantize_q8_1(xs, (char *) y + (size_t) t * (size_t) (k / 32) * 36, k);
+        or_quantize_q8_1(v, (char *) y + (size_t) t * (size_t) (k / 32) * 36, k);
     }
-    free(xs);
+    free(v);
 }
 
 /* ------------------------------------------------------------------ */

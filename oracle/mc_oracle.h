@@ -131,12 +131,15 @@ int or_cpu_mul_mat_id_f32(int type, int64_t ne00, int64_t ne01, int32_t n_as,
                           float *dst, int64_t dst_stride_col, int64_t dst_stride_channel,
                           int32_t nthreads);
 
-/* MoE output combine + (RMS-normalized) q8_1 quantization (the GPU's fused combine kernel):
- * x[t][i] = residual + shared + sum_j w[t][j]*o[t][j][i], accumulated left to right with fmaf;
- * y[t] = q8_1(x[t] * s), s = rms_norm ? 1/sqrtf(mean(x^2) + eps) : 1 (sum order documented in mc_oracle.c). */
+/* MoE output combine + RMSNorm + q8_1 quantization (the GPU's fused combine kernel):
+ * x[t][i] = residual + shared + sum_j w[t][j]*o[t][j][i], accumulated left to right with fmaf (x_out required);
+ * rms_norm: s = 1/sqrtf(or_rms_sum(x[t])/k + eps), v = (x*s)*norm_weight[i] (weight optional); else v = x;
+ * y[t] = q8_1(v). */
 void or_combine_q8_1(const float *o, int64_t o_stride, const float *w, int32_t n_used, const float *shared,
                      int64_t shared_stride, const float *residual, float *x_out, void *y, int64_t k, int64_t n_tok,
-                     int32_t rms_norm, float eps);
+                     int32_t rms_norm, const float *norm_weight, float eps);
+/* Sum of squares of k values (k % 256 == 0) in the GPU kernels' fixed order (mc_oracle.c). */
+float or_rms_sum(const float *x, int64_t k);
 
 /* Deterministic generator used by the synthetic workloads (splitmix64 + Box-Muller). */
 uint64_t or_splitmix64(uint64_t *state);

@@ -82,7 +82,8 @@ def lib():
         L.or_fill_normal.argtypes, L.or_fill_normal.restype = [C.c_uint64, C.c_float, C.c_float, vp, i64], None
         L.or_topk_uniform.argtypes, L.or_topk_uniform.restype = [C.c_uint64, C.c_int32, C.c_int32, C.c_int32, vp], None
         L.or_omp_max_threads.argtypes, L.or_omp_max_threads.restype = [], C.c_int
-        L.or_combine_q8_1.argtypes = [vp, i64, vp, C.c_int32, vp, i64, vp, vp, vp, i64, i64, C.c_int32, C.c_float]
+        L.or_combine_q8_1.argtypes = [vp, i64, vp, C.c_int32, vp, i64, vp, vp, vp, i64, i64, C.c_int32, vp, C.c_float]
+        L.or_rms_sum.argtypes, L.or_rms_sum.restype = [vp, i64], C.c_float
         L.or_combine_q8_1.restype = None
         _lib = L
     return _lib
@@ -279,8 +280,9 @@ def cpu_cores() -> int:
         return os.cpu_count() or 1
 
 
-def combine_q8_1(o, w, shared=None, residual=None, rms_norm=False, eps=1e-6):
-    """o [n_tok, n_used, k], w [n_tok, n_used] -> (x [n_tok, k], q8_1 bytes [n_tok, k/32*36])."""
+def combine_q8_1(o, w, shared=None, residual=None, rms_norm=False, norm_weight=None, eps=1e-6):
+    """o [n_tok, n_used, k], w [n_tok, n_used] -> (x [n_tok, k], q8_1 bytes [n_tok, k/32*36]);
+    with rms_norm the quantized row is (x * rms scale) * norm_weight."""
     o = np.ascontiguousarray(o, dtype=np.float32)
     w = np.ascontiguousarray(w, dtype=np.float32)
     n_tok, n_used, k = o.shape
@@ -288,6 +290,12 @@ def combine_q8_1(o, w, shared=None, residual=None, rms_norm=False, eps=1e-6):
     y = np.empty((n_tok, k // 32 * 36), np.uint8)
     sh = None if shared is None else np.ascontiguousarray(shared, dtype=np.float32)
     res = None if residual is None else np.ascontiguousarray(residual, dtype=np.float32)
+    nw = None if norm_weight is None else np.ascontiguousarray(norm_weight, dtype=np.float32)
     lib().or_combine_q8_1(o.ctypes.data, k, w.ctypes.data, n_used, _p(sh), k, _p(res), x.ctypes.data, y.ctypes.data,
-                          k, n_tok, 1 if rms_norm else 0, eps)
+                          k, n_tok, int(bool(rms_norm)), _p(nw), eps)
     return x, y
+
+
+def rms_sum(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return lib().or_rms_sum(x.ctypes.data, x.size)

@@ -55,14 +55,15 @@ def test_decode_layer_stagewise(torch_gpu, mc, O, small_model):
     assert O.rel_l2(o, want_o[0]) <= 1e-5
     assert O.rel_l2(osh, want_osh) <= 1e-5
 
-    for norm in (False, True):
+    nw = m.norm[1]
+    for norm, weight in ((False, None), (True, None), (True, nw)):
         mc.combine_q8_1(m.o.view(1, U, H), m.w[0], shared=m.o_sh, residual=m.x, x_out=m.x_next, y=m.y,
-                        rms_norm=norm, eps=1e-6)
+                        rms_norm=norm, norm_weight=weight, eps=1e-6)
         torch.cuda.synchronize()
         wx, wy = O.combine_q8_1(o.reshape(1, U, H), w[0, 0].reshape(1, U), shared=osh, residual=x0, rms_norm=norm,
-                                eps=1e-6)
+                                norm_weight=None if weight is None else weight.cpu().numpy(), eps=1e-6)
         assert np.array_equal(m.x_next.cpu().numpy(), wx)
-        assert np.array_equal(m.y.cpu().numpy(), wy), f"rms_norm={norm}"
+        assert np.array_equal(m.y.cpu().numpy(), wy), (norm, weight is not None)
 
 
 def test_decode_graph_replay_matches_eager(torch_gpu, mc, small_model):

@@ -83,12 +83,29 @@ def test_combine_against_numpy():
     w = rng.uniform(0, 1, (2, 5)).astype(np.float32)
     sh = rng.standard_normal((2, 1024)).astype(np.float32)
     res = rng.standard_normal((2, 1024)).astype(np.float32)
-    x, y = O.combine_q8_1(o, w, shared=sh, residual=res, rms_norm=True, eps=1e-6)
+    nw = rng.uniform(0.5, 1.5, 1024).astype(np.float32)
+    x, y = O.combine_q8_1(o, w, shared=sh, residual=res)
     want = res.astype(np.float64) + sh + (w[:, :, None].astype(np.float64) * o).sum(1)
     assert np.allclose(x, want, rtol=1e-6, atol=1e-5)
+    x2, yn = O.combine_q8_1(o, w, shared=sh, residual=res, rms_norm=True, eps=1e-6)
+    x3, ynw = O.combine_q8_1(o, w, shared=sh, residual=res, rms_norm=True, norm_weight=nw, eps=1e-6)
+    assert np.array_equal(x, x2) and np.array_equal(x, x3)
     for t in range(2):
-        s = 1.0 / np.sqrt((x[t].astype(np.float64) ** 2).mean() + 1e-6)
-        deq = O.dequantize(O.Q8_1, y[t], 1024)[0]
-        assert O.rel_l2(deq, x[t] * s) < 0.01
-        _, y_plain = O.combine_q8_1(o[t:t + 1], w[t:t + 1], shared=sh[t:t + 1], residual=res[t:t + 1])
-        assert np.array_equal(y_plain[0], O.quantize_q8_1(x[t]))
+        assert np.array_equal(y[t], O.quantize_q8_1(x[t]))
+        ss = float((x[t].astype(np.float64) ** 2).sum())
+        assert abs(O.rms_sum(x[t]) - ss) <= 1e-5 * ss
+        s64 = 1.0 / np.sqrt(ss / 1024 + 1e-6)
+        # the normalized rows: rms 1 (times the weight), within the q8_1 resolution
+        for q, ref in ((yn[t], x[t] * s64), (ynw[t], x[t] * s64 * nw)):
+            deq = O.dequantize(O.Q8_1, q, 1024)[0]
+            assert O.rel_l2(deq, ref) < 0.01
+        # exactly q8_1 of (x * s) * weight with s from the canonical sum
+        s32 = np.float32(1.0) / np.sqrt(np.float32(O.rms_sum(x[t]) / np.float32(1024) + np.float32(1e-6)))
+        assert np.array_equal(ynw[t], O.quantize_q8_1((x[t] * s32) * nw))
+    # the fixed summation order: chunk sums of 256 values added in order
+    xt = x[0]
+    chunks = [O.rms_sum(xt[256 * j:256 * j + 256]) for j in range(4)]
+    total = np.float32(0)
+    for c in chunks:
+        total = np.float32(total + np.float32(c))
+    assert O.rms_sum(xt) == total
