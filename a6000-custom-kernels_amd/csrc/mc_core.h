@@ -52,25 +52,9 @@ struct Act {
     int s16[UE / 16];
 };
 
-template <int UE, int ACT>
-__device__ __forceinline__ void load_act(Act<UE> &A, __amdgpu_buffer_rsrc_t r, u32 row_off, int col) {
-    if constexpr (ACT == ACT_Q8_1) {
-#pragma unroll
-        for (int b = 0; b < UE / 32; ++b) {
-            const u32 off = row_off + (u32) (col * (UE / 32) + b) * 36u;
-            A.d[b] = h2f(bload(r, off));
-#pragma unroll
-            for (int k = 0; k < 8; ++k) A.q[8 * b + k] = bload(r, off + 4u + 4u * k);
-        }
-    } else {
-        static_assert(UE == 256, "q8_K activations pair with 256-value units");
-        const u32 off = row_off + (u32) col * 292u;
-        const float d = __builtin_bit_cast(float, bload(r, off));
-#pragma unroll
-        for (int b = 0; b < 8; ++b) A.d[b] = d;
-#pragma unroll
-        for (int k = 0; k < 64; ++k) A.q[k] = bload(r, off + 4u + 4u * k);
-    }
+// Sums of each 16 int8 activation values (the min/offset terms of the dots).
+template <int UE>
+__device__ __forceinline__ void act_sums(Act<UE> &A) {
 #pragma unroll
     for (int s = 0; s < UE / 16; ++s) {
         int t = sdot4(A.q[4 * s + 0], 0x01010101u, 0);
@@ -78,6 +62,49 @@ __device__ __forceinline__ void load_act(Act<UE> &A, __amdgpu_buffer_rsrc_t r, u
         t = sdot4(A.q[4 * s + 2], 0x01010101u, t);
         A.s16[s] = sdot4(A.q[4 * s + 3], 0x01010101u, t);
     }
+}
+
+typedef u32 v4u __attribute__((ext_vector_type(4)));
+
+// The lane's activation slice from an LDS copy of its row: UE/32 q8_1 blocks of
+// 36 bytes, or one 292-byte q8_K block, at p (4-byte aligned).  When p is 16-byte
+// aligned (q8_1 slices of 256 values are 288 bytes: 18 chunks) the slice is read
+// with 128-bit LDS reads, else with 32-bit reads.
+template <int UE, int ACT>
+__device__ __forceinline__ void load_act_lds(Act<UE> &A, const uint8_t *p) {
+    constexpr int NW = ACT == ACT_Q8_1 ? UE / 32 * 9 : 73;
+    u32 w[NW];
+    if (NW % 4 == 0 && ((uintptr_t) p & 15u) == 0) {
+        const v4u *q = (const v4u *) __builtin_assume_aligned(p, 16);
+#pragma unroll
+        for (int i = 0; i < NW / 4; ++i) {
+            const v4u v = q[i];
+            w[4 * i] = v.x;
+            w[4 * i + 1] = v.y;
+            w[4 * i + 2] = v.z;
+            w[4 * i + 3] = v.w;
+        }
+    } else {
+        const u32 *q = (const u32 *) p;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) w[i] = q[i];
+    }
+    if constexpr (ACT == ACT_Q8_1) {
+#pragma unroll
+        for (int b = 0; b < UE / 32; ++b) {
+            A.d[b] = h2f(w[9 * b]);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) A.q[8 * b + k] = w[9 * b + 1 + k];
+        }
+    } else {
+        static_assert(UE == 256, "q8_K activations pair with 256-value units");
+        const float d = __builtin_bit_cast(float, w[0]);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) A.d[b] = d;
+#pragma unroll
+        for (int k = 0; k < 64; ++k) A.q[k] = w[1 + k];
+    }
+    act_sums(A);
 }
 
 // ---------------------------------------------------------------------------
@@ -89,6 +116,30 @@ struct WordsAligned {            // unit starts on a 4-byte boundary
     __device__ __forceinline__ u32 operator[](int i) const { return p[i]; }
 };
 
+template <int NW>
+struct WordsRegs {               // unit already in registers
+    u32 w[NW];
+    __device__ __forceinline__ u32 operator[](int i) const { return w[i]; }
+};
+
+// A 16-byte aligned unit of NW words read from LDS with 128-bit reads: units whose
+// size is an odd number of 16-byte chunks (Q4_K 9, Q5_K 11) then hit distinct bank
+// groups in every 8-lane phase, where 32-bit reads at that stride conflict 8 ways.
+template <int NW>
+__device__ __forceinline__ WordsRegs<NW> lds_unit_b128(const uint8_t *p) {
+    WordsRegs<NW> r;
+    const v4u *q = (const v4u *) __builtin_assume_aligned(p, 16);
+#pragma unroll
+    for (int i = 0; i < NW / 4; ++i) {
+        const v4u v = q[i];
+        r.w[4 * i] = v.x;
+        r.w[4 * i + 1] = v.y;
+        r.w[4 * i + 2] = v.z;
+        r.w[4 * i + 3] = v.w;
+    }
+    return r;
+}
+
 struct WordsShifted {            // unit starts on a 2-byte boundary: realign with v_alignbyte
     const u32 *p;
     u32 sh;                      // byte shift 0..3
@@ -98,6 +149,10 @@ struct WordsShifted {            // unit starts on a 2-byte boundary: realign wi
 // ---------------------------------------------------------------------------
 // per-type unit dot products
 // ---------------------------------------------------------------------------
+
+// Integer scale products use 24-bit multiplies (full rate): every integer
+// partial sum below is bounded by 16 * 63 * 127 < 2^23 in magnitude and every
+// sub-block scale by 128, so the products are exact.
 
 // Q2_K: scales[16] | qs[64] | d | dmin.  Element i = 128h + 32j + l uses
 // (qs[32h + l] >> 2j) & 3 and sub-block scale byte i >> 4 (lo 4: scale, hi 4: min).
@@ -130,8 +185,8 @@ __device__ __forceinline__ float dot_q2_K(const W &w, const Act<256> &A) {
             }
             const u32 b0 = byte_of(sc[(2 * g) >> 2], (2 * g) & 3);
             const u32 b1 = byte_of(sc[(2 * g + 1) >> 2], (2 * g + 1) & 3);
-            const int is = (int) (b0 & 0xF) * d0 + (int) (b1 & 0xF) * d1;
-            const int ms = (int) (b0 >> 4) * A.s16[2 * g] + (int) (b1 >> 4) * A.s16[2 * g + 1];
+            const int is = __mul24((int) (b0 & 0xF), d0) + __mul24((int) (b1 & 0xF), d1);
+            const int ms = __mul24((int) (b0 >> 4), A.s16[2 * g]) + __mul24((int) (b1 >> 4), A.s16[2 * g + 1]);
             if constexpr (ACT == ACT_Q8_K) {
                 isum += is >> (2 * jj);
                 msum += ms;
@@ -190,7 +245,7 @@ __device__ __forceinline__ float dot_q3_K(const W &w, const Act<256> &A) {
             const int s0 = 2 * g, s1 = 2 * g + 1;
             const int sc0 = (int) byte_of(S[s0 >> 2], s0 & 3) - 32;
             const int sc1 = (int) byte_of(S[s1 >> 2], s1 & 3) - 32;
-            const int is = sc0 * d0 + sc1 * d1;
+            const int is = __mul24(sc0, d0) + __mul24(sc1, d1);
             if constexpr (ACT == ACT_Q8_K) isum += is;
             else acc = fmaf(A.d[g], (float) is, acc);
         }
@@ -244,8 +299,8 @@ __device__ __forceinline__ float dot_q45_K(const W &w, const Act<256> &A) {
             }
             const int sc = (int) byte_of(g < 4 ? SC0 : SC1, g & 3);
             const int m = (int) byte_of(g < 4 ? M0 : M1, g & 3);
-            const int is = sc * dot;
-            const int ms = m * (A.s16[2 * g] + A.s16[2 * g + 1]);
+            const int is = __mul24(sc, dot);
+            const int ms = __mul24(m, A.s16[2 * g] + A.s16[2 * g + 1]);
             if constexpr (ACT == ACT_Q8_K) {
                 isum += is;
                 msum += ms;
@@ -297,7 +352,7 @@ __device__ __forceinline__ float dot_q6_K(const W &w, const Act<256> &A) {
             const int s0 = 2 * g, s1 = 2 * g + 1;
             const int sc0 = (int) (int8_t) byte_of(sc[s0 >> 2], s0 & 3);
             const int sc1 = (int) (int8_t) byte_of(sc[s1 >> 2], s1 & 3);
-            const int is = sc0 * d0 + sc1 * d1;
+            const int is = __mul24(sc0, d0) + __mul24(sc1, d1);
             if constexpr (ACT == ACT_Q8_K) isum += is;
             else acc = fmaf(A.d[g], (float) is, acc);
         }
@@ -402,9 +457,11 @@ __device__ __forceinline__ float glu_apply(int op, float g, float up, float limi
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
+// Streams [start, start + nbytes) of the matrix at `base` into lds (lds[x] = byte
+// (start & ~15) + x of the 16-byte aligned view); returns the number of DMA
+// instructions issued (one per KiB).
 template <int T>
-__device__ __forceinline__ void dma_span(const uint8_t *base, u32 base_bytes, u32 start, u32 nbytes, uint8_t *lds) {
-    // stream [start, start + nbytes) of the matrix at `base` into lds: lds[x] = byte (start & ~15) + x
+__device__ __forceinline__ int dma_span(const uint8_t *base, u32 base_bytes, u32 start, u32 nbytes, uint8_t *lds) {
     const uintptr_t abase = (uintptr_t) base & ~(uintptr_t) 15;
     const u32 skew = (u32) ((uintptr_t) base - abase);
     const __amdgpu_buffer_rsrc_t r = make_rsrc((const void *) abase, base_bytes + skew);
@@ -412,13 +469,64 @@ __device__ __forceinline__ void dma_span(const uint8_t *base, u32 base_bytes, u3
     const u32 lead = (start + skew) - a0;
     const int rounds = (int) ((lead + nbytes + 1023u) >> 10);
     constexpr int MAXR = span_lds_bytes(T) / 1024;
-    const u32 lane_off = a0 + 16u * threadIdx.x;
+    const u32 lane_off = a0 + 16u * (threadIdx.x % WAVE);
 #pragma unroll
     for (int i = 0; i < MAXR; ++i) {
         if (i < rounds) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * i), 16, lane_off + 1024u * i, 0, 0, 0);
         }
     }
+    return rounds;
+}
+
+// Waits until at most n of this wave's vector memory loads are outstanding
+// (loads complete in issue order, so every earlier load has landed).
+__device__ __forceinline__ void wait_loads_at_most(int n) {
+    switch (n) {
+#define MC_WAITCASE(k) case k: asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); break;
+        MC_WAITCASE(0) MC_WAITCASE(1) MC_WAITCASE(2) MC_WAITCASE(3) MC_WAITCASE(4) MC_WAITCASE(5)
+        MC_WAITCASE(6) MC_WAITCASE(7) MC_WAITCASE(8) MC_WAITCASE(9) MC_WAITCASE(10) MC_WAITCASE(11)
+        MC_WAITCASE(12) MC_WAITCASE(13) MC_WAITCASE(14)
+#undef MC_WAITCASE
+        default: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
+    }
+}
+
+// Uniform loads through the scalar data cache (read-only data: routing ids and
+// pointer tables, which no kernel writes while it runs).
+template <class V>
+__device__ __forceinline__ V sload(const V *p) {
+    return *(const __attribute__((address_space(4))) V *) p;
+}
+
+// Sum over the nu consecutive lanes of each row group (lane r*nu .. r*nu+nu-1):
+// xor butterfly when nu is a power of two (total in every lane of the group),
+// else lane r*nu adds lanes r*nu+1 .. r*nu+nu-1 in order (total in lane r*nu).
+__device__ __forceinline__ float row_group_sum(float v, int nu) {
+    if ((nu & (nu - 1)) == 0) {
+        for (int off = nu >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, WAVE);
+        return v;
+    }
+    float s = v;
+    for (int i = 1; i < nu; ++i) s += __shfl_down(v, (unsigned) i, WAVE);
+    return s;
+}
+
+// Streams bytes [off, off + nbytes) of `base` (a buffer of base_bytes bytes) into
+// LDS with 16-byte buffer->LDS DMA loads from the 16-byte aligned address at or
+// below base + off.  Returns the lead: byte `off` lands at lds[lead] (lead < 16).
+// The LDS destination must hold round_up_1k(lead + nbytes) bytes.
+__device__ __forceinline__ u32 dma_bytes(const uint8_t *base, u32 base_bytes, u32 off, u32 nbytes, uint8_t *lds) {
+    const uintptr_t abase = (uintptr_t) base & ~(uintptr_t) 15;
+    const u32 skew = (u32) ((uintptr_t) base - abase);
+    const __amdgpu_buffer_rsrc_t r = make_rsrc((const void *) abase, base_bytes + skew);
+    const u32 a0 = (off + skew) & ~15u;
+    const u32 lead = (off + skew) - a0;
+    const int rounds = (int) ((lead + nbytes + 1023u) >> 10);
+    const u32 lane_off = a0 + 16u * (threadIdx.x % WAVE);
+    for (int i = 0; i < rounds; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * i), 16, lane_off + 1024u * i, 0, 0, 0);
+    return lead;
 }
 
 // Byte offset, inside the LDS copy made by dma_span, of byte `start` of the matrix at `base`.
@@ -433,6 +541,9 @@ __device__ __forceinline__ float span_unit_dot(const uint8_t *lds_span, u32 lead
                                                const Act<type_geom(T).unit_elems> &A) {
     constexpr TypeGeom G = type_geom(T);
     const u32 uoff = lead + (u32) unit * G.unit_bytes;
+    if constexpr (G.aligned && G.unit_bytes % 16 == 0) {
+        if ((uoff & 15u) == 0) return unit_dot<T, ACT>(lds_unit_b128<G.unit_bytes / 4>(lds_span + uoff), A);
+    }
     if constexpr (G.aligned) {
         return unit_dot<T, ACT>(WordsAligned{(const u32 *) (lds_span + uoff)}, A);
     } else {
@@ -530,34 +641,6 @@ __device__ __forceinline__ void quantize_chunk(const float *xs, bool norm, float
         uint8_t *yb = y + (i / 32) * 36;
         yb[4 + (lane & 31)] = (uint8_t) q;
         if ((lane & 31) == 0) *(u32 *) yb = (u32) f2h_bits(d) | ((u32) f2h_bits(sum) << 16);
-    }
-}
-
-// q8_1 codes and scales of a row of k fp32 values (k % 64 == 0) into LDS with the
-// arithmetic of the q8_1 quantizer: codes[i] int8, dsc[b] = the block's fp16 scale as float.
-__device__ __forceinline__ void quantize_row_to_lds(const float *x, int k, int8_t *codes, float *dsc) {
-    const int lane = threadIdx.x % WAVE;
-    for (int base = 0; base < k; base += WAVE) {
-        float d, sum;
-        const int8_t q = q8_1_lane(x[base + lane], d, sum);
-        codes[base + lane] = q;
-        if ((lane & 31) == 0) dsc[(base + lane) / 32] = h2f(f2h_bits(d));
-    }
-}
-
-// The lane's 256-value activation slice `col` from quantize_row_to_lds output.
-__device__ __forceinline__ void load_act_lds(Act<256> &A, const int8_t *codes, const float *dsc, int col) {
-    const u32 *cw = (const u32 *) (codes + col * 256);
-#pragma unroll
-    for (int k = 0; k < 64; ++k) A.q[k] = cw[k];
-#pragma unroll
-    for (int b = 0; b < 8; ++b) A.d[b] = dsc[col * 8 + b];
-#pragma unroll
-    for (int s = 0; s < 16; ++s) {
-        int t = sdot4(A.q[4 * s + 0], 0x01010101u, 0);
-        t = sdot4(A.q[4 * s + 1], 0x01010101u, t);
-        t = sdot4(A.q[4 * s + 2], 0x01010101u, t);
-        A.s16[s] = sdot4(A.q[4 * s + 3], 0x01010101u, t);
     }
 }
 

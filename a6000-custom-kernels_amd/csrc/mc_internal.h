@@ -109,12 +109,29 @@ struct GemvArgs {
     int32_t nrows;                // rows per expert (ne01)
     int32_t n_used;               // picks per token (nchannels_dst)
     int32_t n_tok;                // tokens (ncols_dst)
-    // tiling (filled by the launcher)
+    // tiling and LDS layout (filled by the launcher)
+    int32_t rps;                  // rows per step of a routed matrix
+    int32_t sh_rps;               // rows per step of the shared matrix
     int32_t tiles_per_pick;
     int32_t sh_tiles_per_tok;
     int32_t n_routed_tiles;
     int32_t n_tiles;
+    int32_t rec;                  // 1: workgroup 0 is the pick recorder, tiles start at 1
+    uint32_t act_row_bytes;       // bytes of one activation row
+    uint32_t lds_span;            // LDS bytes per staged matrix span (up at 0, gate at lds_span)
+    uint32_t lds_act;             // LDS offset of the staged activation row
+    uint32_t lds_red;             // LDS offset of the 64-float reduction scratch
+    uint32_t lds_total;           // dynamic LDS bytes per workgroup
 };
+
+// LDS a GEMV workgroup may use, chosen so that 8 workgroups fit one CU's
+// 160 KiB: a decode launch of ~2000 single-wave tiles is then resident at once.
+constexpr uint32_t GEMV_LDS_BUDGET = 20 * 1024;
+
+inline constexpr uint32_t round_up_1k(uint32_t b) { return (b + 1023u) & ~1023u; }
+
+// LDS bytes staging `rows` rows of `row_bytes` (16-byte lead-in + 4-byte over-read, whole 1 KiB DMA rounds).
+inline constexpr uint32_t span_bytes(uint32_t rows, uint32_t row_bytes) { return round_up_1k(rows * row_bytes + 20u); }
 
 struct QuantArgs {
     const float *x;

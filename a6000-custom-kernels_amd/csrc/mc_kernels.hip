@@ -86,41 +86,31 @@ __device__ void record_picks(const GemvArgs &a) {
 // one step of one matrix pair (up [+ gate]) for one pick
 // ---------------------------------------------------------------------------
 template <int T, int ACT>
-__device__ __forceinline__ void run_step(const GemvArgs &a, uint8_t *lds, float *red, bool shared, int tile) {
+__device__ __forceinline__ void run_step(const GemvArgs &a, uint8_t *lds, bool shared, int tile) {
     constexpr TypeGeom G = type_geom(T);
     constexpr int UE = G.unit_elems, UB = G.unit_bytes;
-    constexpr int SPAN = span_lds_bytes(T);
+    constexpr int AUB = ACT == ACT_Q8_1 ? UE / 32 * 36 : 292;   // activation bytes per unit
     const int lane = threadIdx.x;
     const int K = a.ncols;
     const int nu = K / UE;                   // units per row (<= 64, checked on the host)
-    const int rps = WAVE / nu;               // rows per step
+    const int rps = shared ? a.sh_rps : a.rps;
     const u32 RB = (u32) nu * UB;            // row bytes
 
-    int t, c = 0, e = 0, row0;
-    const uint8_t *wup, *wgate = nullptr;
-    u32 mbytes;
+    // the activation row depends only on (token, slot): its DMA goes out first
+    int t, c = 0, row0, pick = 0;
     const uint8_t *ybase;
     u32 yrow, ybytes;
     if (!shared) {
-        const int pick = tile / a.tiles_per_pick;
+        pick = tile / a.tiles_per_pick;
         row0 = (tile % a.tiles_per_pick) * rps;
         t = pick / a.n_used;
         c = pick % a.n_used;
-        e = a.ids[c + (int64_t) t * a.ids_stride];
-        if (e < 0 || e >= a.n_experts) return;
-        wup = (const uint8_t *) (uintptr_t) (a.tbl[e] & ~(uint64_t) 1);
-        if (a.has_gate) wgate = (const uint8_t *) (uintptr_t) (a.tbl_gate[e] & ~(uint64_t) 1);
-        mbytes = (u32) a.expert_bytes;
         ybase = a.y;
         ybytes = (u32) a.y_bytes;
         yrow = (u32) ((int64_t) (c % (int) a.nchannels_y) * a.stride_channel_y + (int64_t) t * a.stride_col_y);
     } else {
-        const int st = tile - a.n_routed_tiles;
-        t = st / a.sh_tiles_per_tok;
-        row0 = (st % a.sh_tiles_per_tok) * rps;
-        wup = a.sh_up;
-        wgate = a.sh_gate;
-        mbytes = (u32) a.sh_matrix_bytes;
+        t = tile / a.sh_tiles_per_tok;
+        row0 = (tile % a.sh_tiles_per_tok) * rps;
         if (a.sh_y) {
             ybase = a.sh_y;
             ybytes = (u32) a.sh_y_bytes;
@@ -131,33 +121,57 @@ __device__ __forceinline__ void run_step(const GemvArgs &a, uint8_t *lds, float 
             yrow = (u32) ((int64_t) t * a.stride_col_y);
         }
     }
+    const u32 alead = dma_bytes(ybase, ybytes, yrow, a.act_row_bytes, lds + a.lds_act);
+
+    // resolve the weights: expert id and tagged table entries through the scalar cache
+    int e = 0;
+    const uint8_t *wup, *wgate = nullptr;
+    u32 mbytes;
+    if (!shared) {
+        e = sload(a.ids + c + (int64_t) t * a.ids_stride);
+        if (e < 0 || e >= a.n_experts) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            return;
+        }
+        wup = (const uint8_t *) (uintptr_t) (sload(a.tbl + e) & ~(uint64_t) 1);
+        if (a.has_gate) wgate = (const uint8_t *) (uintptr_t) (sload(a.tbl_gate + e) & ~(uint64_t) 1);
+        mbytes = (u32) a.expert_bytes;
+    } else {
+        wup = a.sh_up;
+        wgate = a.sh_gate;
+        mbytes = (u32) a.sh_matrix_bytes;
+    }
     const int nrows_here = min(rps, a.nrows - row0);
     const u32 start = (u32) row0 * RB, nbytes = (u32) nrows_here * RB;
 
-    // issue the weight DMA first (it does not depend on the activations)
-    dma_span<T>(wup, mbytes, start, nbytes, lds);
-    if (wgate) dma_span<T>(wgate, mbytes, start, nbytes, lds + SPAN);
+    // gate span, then up span; the gate dot runs while the up span is landing
+    if (wgate) dma_span<T>(wgate, mbytes, start, nbytes, lds + a.lds_span);
+    const int n_up = dma_span<T>(wup, mbytes, start, nbytes, lds);
 
-    // this lane's activation slice (column `col` of the row)
     const int row_local = lane / nu, col = lane % nu;
     const bool active = row_local < nrows_here;
+    const int unit = row_local * nu + col;
+    const uint8_t *aslice = lds + a.lds_act + alead + (u32) col * AUB;
     Act<UE> A;
-    {
-        const __amdgpu_buffer_rsrc_t ry = make_rsrc(ybase, ybytes);
-        load_act<UE, ACT>(A, ry, yrow, col);
-    }
-
-    // the DMA writes LDS asynchronously; wait for it before reading
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-
     float pu = 0.0f, pg = 0.0f;
-    if (active) {
-        pu = span_unit_dot<T, ACT>(lds, span_lead(wup, start), row_local * nu + col, A);
-        if (wgate) pg = span_unit_dot<T, ACT>(lds + SPAN, span_lead(wgate, start), row_local * nu + col, A);
+    if (wgate) {
+        wait_loads_at_most(n_up);            // activation and gate span have landed
+        if (active) {
+            load_act_lds<UE, ACT>(A, aslice);
+            pg = span_unit_dot<T, ACT>(lds + a.lds_span, span_lead(wgate, start), unit, A);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (active) pu = span_unit_dot<T, ACT>(lds, span_lead(wup, start), unit, A);
+    } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (active) {
+            load_act_lds<UE, ACT>(A, aslice);
+            pu = span_unit_dot<T, ACT>(lds, span_lead(wup, start), unit, A);
+        }
     }
-    // row sums in a fixed order (lane r*nu adds the nu partials of row r left to right)
-    float su = step_row_sum(red, pu, nu);
-    float sg = wgate ? step_row_sum(red, pg, nu) : 0.0f;
+    // row sums across the nu lanes of each row (cross-lane adds, no LDS)
+    const float su = row_group_sum(pu, nu);
+    const float sg = wgate ? row_group_sum(pg, nu) : 0.0f;
     if (active && col == 0) {
         const int row = row0 + row_local;
         float out;
@@ -180,17 +194,22 @@ __device__ __forceinline__ void run_step(const GemvArgs &a, uint8_t *lds, float 
     }
 }
 
+// One wave per workgroup.  Workgroup 0 is the pick recorder when anything is
+// recorded; then the shared-expert steps (the heaviest, dispatched first), then
+// the routed steps.  Dynamic LDS: [up span | gate span | activation row | scratch].
 template <int TW, int TS, int ACT>
 __global__ __launch_bounds__(WAVE) void mc_gemv_kernel(const GemvArgs a) {
-    constexpr int SPAN = span_lds_bytes(TW) > span_lds_bytes(TS) ? span_lds_bytes(TW) : span_lds_bytes(TS);
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * SPAN + 16];
-    __shared__ float red[2 * WAVE + 64];
-    if (blockIdx.x == 0) record_picks(a);
-    const int tile = blockIdx.x;
-    if (tile < a.n_routed_tiles) {
-        run_step<TW, ACT>(a, lds, red, false, tile);
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    if (a.rec && blockIdx.x == 0) {
+        record_picks(a);
+        return;
+    }
+    const int tile = (int) blockIdx.x - a.rec;
+    const int n_sh = a.sh_tiles_per_tok * a.n_tok;
+    if (tile >= n_sh) {
+        run_step<TW, ACT>(a, lds, false, tile - n_sh);
     } else if constexpr (TS != 0) {
-        run_step<TS, ACT>(a, lds, red, true, tile);
+        run_step<TS, ACT>(a, lds, true, tile);
     }
 }
 
@@ -351,7 +370,8 @@ __global__ __launch_bounds__(COMBINE_THREADS) void mc_combine_q8_1_kernel(const 
 
 template <int TW, int TS, int ACT>
 static hipError_t launch_t(const GemvArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL((mc_gemv_kernel<TW, TS, ACT>), dim3((unsigned) a.n_tiles), dim3(WAVE), 0, s, a);
+    hipLaunchKernelGGL((mc_gemv_kernel<TW, TS, ACT>), dim3((unsigned) (a.n_tiles + a.rec)), dim3(WAVE),
+                       a.lds_total, s, a);
     return hipGetLastError();
 }
 
@@ -391,21 +411,44 @@ static hipError_t launch_act(const GemvArgs &a, int ts, int act, hipStream_t s) 
     return hipErrorInvalidValue;
 }
 
-// Fills the tiling fields of `a` and launches.  Returns a hipError_t value.
+// Rows per step for a matrix with nu units of row_bytes per row: the most rows
+// (<= 64 / nu) whose staged spans (nspan of them) fit GEMV_LDS_BUDGET beside the
+// activation row.
+static int fit_rows_per_step(int nu, uint32_t row_bytes, int nspan, uint32_t act_span) {
+    int r = WAVE / nu;
+    while (r > 1 && nspan * span_bytes((uint32_t) r, row_bytes) + act_span + 256u > GEMV_LDS_BUDGET) --r;
+    return r;
+}
+
+// Fills the tiling and LDS fields of `a` and launches.  Returns a hipError_t value.
 int launch_gemv(GemvArgs a, int tw, int ts, int act, void *stream) {
     const TypeGeom g = type_geom(tw);
     const int nu = a.ncols / g.unit_elems;
-    const int rps = WAVE / nu;
-    a.tiles_per_pick = (a.nrows + rps - 1) / rps;
+    const uint32_t rb = (uint32_t) nu * (uint32_t) g.unit_bytes;
+    a.act_row_bytes = act == ACT_Q8_1 ? (uint32_t) (a.ncols / 32 * 36) : (uint32_t) (a.ncols / 256 * 292);
+    const uint32_t act_span = round_up_1k(a.act_row_bytes + 20u);
+    if (ts == 0 || !a.sh_up) ts = 0;
+    const int nspan = (a.has_gate || (ts != 0 && a.sh_gate)) ? 2 : 1;
+    a.rps = fit_rows_per_step(nu, rb, nspan, act_span);
+    a.tiles_per_pick = (a.nrows + a.rps - 1) / a.rps;
     a.n_routed_tiles = a.tiles_per_pick * a.n_used * a.n_tok;
+    uint32_t span = span_bytes((uint32_t) a.rps, rb);
+    a.sh_rps = 0;
     a.sh_tiles_per_tok = 0;
-    if (ts != 0 && a.sh_up) {
-        const int nus = a.ncols / type_geom(ts).unit_elems;
-        const int rpss = WAVE / nus;
-        a.sh_tiles_per_tok = (a.nrows + rpss - 1) / rpss;
-    } else {
-        ts = 0;
+    if (ts != 0) {
+        const TypeGeom gs = type_geom(ts);
+        const int nus = a.ncols / gs.unit_elems;
+        const uint32_t rbs = (uint32_t) nus * (uint32_t) gs.unit_bytes;
+        a.sh_rps = fit_rows_per_step(nus, rbs, nspan, act_span);
+        a.sh_tiles_per_tok = (a.nrows + a.sh_rps - 1) / a.sh_rps;
+        const uint32_t sspan = span_bytes((uint32_t) a.sh_rps, rbs);
+        span = sspan > span ? sspan : span;
     }
+    a.lds_span = span;
+    a.lds_act = (uint32_t) nspan * span;
+    a.lds_red = a.lds_act + act_span;
+    a.lds_total = a.lds_red + 256u;
+    a.rec = (a.stats || a.stamps || a.stamps_gate) ? 1 : 0;
     a.n_tiles = a.n_routed_tiles + a.sh_tiles_per_tok * a.n_tok;
     if (a.n_tiles <= 0) return (int) hipSuccess;
     hipStream_t s = (hipStream_t) stream;
