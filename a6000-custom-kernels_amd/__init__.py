@@ -28,7 +28,7 @@ TYPE_NAMES = {Q4_0: "q4_0", Q5_0: "q5_0", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_
 # GLU ops
 GLU_REGLU, GLU_GEGLU, GLU_SWIGLU, GLU_SWIGLU_OAI, GLU_GEGLU_ERF, GLU_GEGLU_QUICK, GLU_SWIGLU_CLAMP = range(7)
 # activation formats
-ACT_Q8_1, ACT_Q8_K = 0, 1
+ACT_Q8_1, ACT_Q8_K, ACT_F32 = 0, 1, 2
 
 MISS_CAP = 8190
 STATS_WORDS = 2 + MISS_CAP
@@ -231,7 +231,8 @@ def mul_mat_vec(*, wtype, weights, ids, y, dst, K, R, n_experts, use_cache=False
 
     weights: device uint8 tensor [n_experts, R, row_bytes] (use_cache=False) or a pinned host pointer
     (weights_ptr, use_cache=True); ids: int32 [n_tok, n_used] (device); y: activation blocks,
-    [n_tok, nchannels_y, act_row_bytes] (device); dst: float32 [n_tok, n_used, R] (device).
+    [n_tok, nchannels_y, act_row_bytes] (device), or fp32 rows [n_tok, nchannels_y, K] with act=ACT_F32;
+    dst: float32 [n_tok, n_used, R] (device).
     """
     n_tok, n_used = ids.shape
     _require_gpu(ids, y, dst)
@@ -241,7 +242,7 @@ def mul_mat_vec(*, wtype, weights, ids, y, dst, K, R, n_experts, use_cache=False
     g = None
     if gate_ptr is not None:
         g = make_tensor(wtype, K, R, n_experts, gate_ptr, name=name.replace("up", "gate"), keep=keep)
-    ablk = (32, 36) if act == ACT_Q8_1 else (256, 292)
+    ablk = {ACT_Q8_1: (32, 36), ACT_Q8_K: (256, 292), ACT_F32: (1, 4)}[act]
     act_row = K // ablk[0]
     rc = lib().ggml_hip_moe_mul_mat_vec_ex(
         1 if use_cache else 0, act, C.byref(src0), C.byref(g) if g is not None else None,

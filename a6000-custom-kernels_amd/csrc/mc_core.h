@@ -65,6 +65,7 @@ __device__ __forceinline__ void act_sums(Act<UE> &A) {
 }
 
 typedef u32 v4u __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 // The lane's activation slice from an LDS copy of its row: UE/32 q8_1 blocks of
 // 36 bytes, or one 292-byte q8_K block, at p (4-byte aligned).  When p is 16-byte
@@ -586,35 +587,104 @@ __device__ __forceinline__ int8_t q8_1_lane(float x, float &d, float &sum) {
     return amax == 0.0f ? (int8_t) 0 : (int8_t) roundf(x / d);
 }
 
+// q8_1 blocks of the k fp32 values at x (LDS, 4-byte aligned, k % 32 == 0) into
+// q (LDS, 36-byte blocks, 4-byte aligned) with the arithmetic of the q8_1
+// quantizer: amax over each 32 values, d = amax / 127 (IEEE division),
+// code = amax == 0 ? 0 : roundf(x / d).  Two lanes own one block (16 values
+// each, one partner exchange), so there is no chain of cross-lane reductions.
+// The block's s half is left unset: the dot products read only d and the codes.
+__device__ __forceinline__ void quantize_row_lds(const float *x, uint8_t *q, int k) {
+    const int lane = threadIdx.x % WAVE;
+    const int nblk = k / 32;
+    for (int b0 = 0; b0 < nblk; b0 += WAVE / 2) {
+        const int b = b0 + lane / 2, half = lane & 1;
+        const bool on = b < nblk;
+        float v[16];
+        const float *src = x + (on ? b : 0) * 32 + 16 * half;
+        if (((uintptr_t) x & 15u) == 0) {
+            const v4f *s4 = (const v4f *) __builtin_assume_aligned(src, 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const v4f w = s4[i];
+                v[4 * i] = w.x;
+                v[4 * i + 1] = w.y;
+                v[4 * i + 2] = w.z;
+                v[4 * i + 3] = w.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = src[i];
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+        amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
+        const float d = amax / 127.0f;
+        u32 packed[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            u32 wd = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int code = amax == 0.0f ? 0 : (int) roundf(v[4 * i + j] / d);
+                wd |= ((u32) code & 0xFFu) << (8 * j);
+            }
+            packed[i] = wd;
+        }
+        if (on) {
+            u32 *dst = (u32 *) (q + b * 36 + 4 + 16 * half);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dst[i] = packed[i];
+            if (half == 0) *(u32 *) (q + b * 36) = (u32) f2h_bits(d);   // same access type as the readers
+        }
+    }
+    wave_lds_sync();
+}
+
 constexpr int COMBINE_MAX_USED = 16;
 
-// One 64-lane wave: the 256 combined values of chunk j of a row
+// One 64-lane wave: the 256 combined values of chunk j of a row, lane l holding
+// values 256j + 4l .. 256j + 4l + 3 (16-byte loads; rows 16-byte aligned):
 //   x = residual + shared + sum_c w[c] * o[c]   (c ascending, fmaf)
-// into xs (row-relative index) and x_out (when given); returns the chunk's RMS
-// sum in the canonical order (mc_internal.h) in every lane.
+// into xv (registers) and x_out (when given); returns the chunk's RMS sum in the
+// canonical order (mc_internal.h) in every lane.
 __device__ __forceinline__ float combine_chunk(const float *o, int64_t o_stride, const float *w, int n_used,
-                                               const float *shared, const float *residual, float *x_out, float *xs,
-                                               int j) {
+                                               const float *shared, const float *residual, float *x_out, int j,
+                                               float xv[4]) {
     const int lane = threadIdx.x % WAVE;
+    const int64_t i0 = (int64_t) j * RMS_CHUNK + 4 * lane;
     float wc[COMBINE_MAX_USED];
 #pragma unroll
     for (int c = 0; c < COMBINE_MAX_USED; ++c) wc[c] = c < n_used ? w[c] : 0.0f;
+    v4f ov[COMBINE_MAX_USED];
+#pragma unroll
+    for (int c = 0; c < COMBINE_MAX_USED; ++c)
+        if (c < n_used) ov[c] = *(const v4f *) (o + c * o_stride + i0);
+    v4f x = residual ? *(const v4f *) (residual + i0) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    if (shared) {
+        const v4f sh = *(const v4f *) (shared + i0);
+        x.x += sh.x;
+        x.y += sh.y;
+        x.z += sh.z;
+        x.w += sh.w;
+    }
+#pragma unroll
+    for (int c = 0; c < COMBINE_MAX_USED; ++c) {
+        if (c < n_used) {
+            x.x = fmaf(wc[c], ov[c].x, x.x);
+            x.y = fmaf(wc[c], ov[c].y, x.y);
+            x.z = fmaf(wc[c], ov[c].z, x.z);
+            x.w = fmaf(wc[c], ov[c].w, x.w);
+        }
+    }
+    if (x_out) *(v4f *) (x_out + i0) = x;
+    xv[0] = x.x;
+    xv[1] = x.y;
+    xv[2] = x.z;
+    xv[3] = x.w;
     float a = 0.0f;
 #pragma unroll
-    for (int p = 0; p < RMS_CHUNK / WAVE; ++p) {
-        const int64_t i = (int64_t) j * RMS_CHUNK + WAVE * p + lane;
-        float ov[COMBINE_MAX_USED];
-#pragma unroll
-        for (int c = 0; c < COMBINE_MAX_USED; ++c) ov[c] = c < n_used ? o[c * o_stride + i] : 0.0f;
-        float x = residual ? residual[i] : 0.0f;
-        if (shared) x += shared[i];
-#pragma unroll
-        for (int c = 0; c < COMBINE_MAX_USED; ++c)
-            if (c < n_used) x = fmaf(wc[c], ov[c], x);
-        if (x_out) x_out[i] = x;
-        xs[i] = x;
-        a = fmaf(x, x, a);
-    }
+    for (int k = 0; k < 4; ++k) a = fmaf(xv[k], xv[k], a);
 #pragma unroll
     for (int off = WAVE / 2; off > 0; off >>= 1) {
         const float other = __shfl_down(a, off, WAVE);
@@ -623,25 +693,43 @@ __device__ __forceinline__ float combine_chunk(const float *o, int64_t o_stride,
     return __shfl(a, 0, WAVE);
 }
 
-// One 64-lane wave: q8_1 of the 256 values v of chunk j into y (row base), with
-// v = (xs[i] * s) * nw[i] under norm (nw optional) and v = xs[i] otherwise.
-__device__ __forceinline__ void quantize_chunk(const float *xs, bool norm, float s, const float *nw, uint8_t *y,
+// One 64-lane wave: q8_1 of the 256 values v of chunk j into y (row base), lane l
+// holding values 4l .. 4l+3 of the chunk in xv, with v = (x * s) * nw[i] under norm
+// (nw optional) and v = x otherwise.  Eight lanes form one 32-value block.  The
+// arithmetic is the q8_1 quantizer's (q8_1_lane): amax, d = amax / 127,
+// code = amax == 0 ? 0 : roundf(v / d), and the block sum in the quantizer's
+// xor-butterfly order (offsets 16, 8, 4 across lanes, then 2, 1 inside the lane).
+__device__ __forceinline__ void quantize_chunk(const float xv[4], bool norm, float s, const v4f nwv, uint8_t *y,
                                                int j) {
     const int lane = threadIdx.x % WAVE;
+    float v[4] = {xv[0], xv[1], xv[2], xv[3]};
+    if (norm) {
+        const float nw[4] = {nwv.x, nwv.y, nwv.z, nwv.w};
 #pragma unroll
-    for (int p = 0; p < RMS_CHUNK / WAVE; ++p) {
-        const int i = j * RMS_CHUNK + WAVE * p + lane;
-        float v = xs[i];
-        if (norm) {
-            v *= s;
-            if (nw) v *= nw[i];
-        }
-        float d, sum;
-        const int8_t q = q8_1_lane(v, d, sum);
-        uint8_t *yb = y + (i / 32) * 36;
-        yb[4 + (lane & 31)] = (uint8_t) q;
-        if ((lane & 31) == 0) *(u32 *) yb = (u32) f2h_bits(d) | ((u32) f2h_bits(sum) << 16);
+        for (int k = 0; k < 4; ++k) v[k] = (v[k] * s) * nw[k];
     }
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+    for (int off = 4; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, WAVE));
+    float t[4] = {v[0], v[1], v[2], v[3]};
+#pragma unroll
+    for (int off = 4; off > 0; off >>= 1) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t[k] += __shfl_xor(t[k], off, WAVE);
+    }
+    const float t2[4] = {t[0] + t[2], t[1] + t[3], t[2] + t[0], t[3] + t[1]};
+    const float sum = t2[0] + t2[1];
+    const float d = amax / 127.0f;
+    u32 packed = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int code = amax == 0.0f ? 0 : (int) roundf(v[k] / d);
+        packed |= ((u32) code & 0xFFu) << (8 * k);
+    }
+    const int i = j * RMS_CHUNK + 4 * lane;               // first value of this lane in the row
+    uint8_t *yb = y + (i / 32) * 36;
+    *(u32 *) (yb + 4 + (i % 32)) = packed;
+    if ((lane & 7) == 0) *(u32 *) yb = (u32) f2h_bits(d) | ((u32) f2h_bits(sum) << 16);
 }
 
 }  // namespace mc

@@ -496,7 +496,8 @@ int gemv_common(int use_cache, int act, const ggml_hip_moe_tensor *src0, const g
     if (ne00 / g.unit_elems > WAVE) return fail(E_UNSUPPORTED, "moe-gemv: ne00=%lld exceeds %d units per row", (long long) ne00, WAVE);
     if (src0->ne[0] != ne00 || src0->ne[1] != ne01 || src0->ne[2] != ne02 || !is_contiguous(src0))
         return fail(E_INVALID, "moe-gemv: src0 shape/strides do not match the call");
-    if (act != ACT_Q8_1 && act != ACT_Q8_K) return fail(E_INVALID, "moe-gemv: unknown activation format %d", act);
+    if (act != ACT_Q8_1 && act != ACT_Q8_K && act != ACT_F32)
+        return fail(E_INVALID, "moe-gemv: unknown activation format %d", act);
     if (act == ACT_Q8_K && !g.kquant) return fail(E_UNSUPPORTED, "moe-gemv: q8_K activations need K-quant weights");
     const size_t eb = (size_t) src0->nb[2];
     if (eb > 0xFFFFFFF0ull) return fail(E_UNSUPPORTED, "moe-gemv: expert matrix larger than 4 GiB");
@@ -517,8 +518,10 @@ int gemv_common(int use_cache, int act, const ggml_hip_moe_tensor *src0, const g
     if (!aligned_ok) return fail(E_UNSUPPORTED, "moe-gemv: expert base/size alignment not supported");
 
     GemvArgs a = {};
-    const int ablk_bytes = act == ACT_Q8_1 ? 36 : 292;
-    const int ablk_elems = act == ACT_Q8_1 ? 32 : 256;
+    // strides count activation blocks (q8_1: 32 values, q8_K: 256) or floats (fp32 rows)
+    const int ablk_bytes = act == ACT_Q8_1 ? 36 : act == ACT_Q8_K ? 292 : 4;
+    const int ablk_elems = act == ACT_Q8_1 ? 32 : act == ACT_Q8_K ? 256 : 1;
+    if (act == ACT_F32 && (((uintptr_t) src1) & 3u)) return fail(E_INVALID, "moe-gemv: misaligned fp32 activations");
     if (ne00 % ablk_elems) return fail(E_INVALID, "moe-gemv: ne00 not a multiple of the activation block");
     const int64_t act_row = ne00 / ablk_elems * ablk_bytes;
     a.y = (const uint8_t *) src1;
@@ -754,6 +757,10 @@ int ggml_hip_moe_combine_q8_1(const float *o, int64_t o_stride, const float *w, 
         (shared && shared_stride < k) || y_stride < k / 32)
         return fail(E_INVALID, "combine: bad shape");
     if ((uintptr_t) y_q8_1 & 3u) return fail(E_INVALID, "combine: misaligned output");
+    // the kernel moves 4 floats per lane: rows and strides on 16-byte boundaries
+    if ((((uintptr_t) o | (uintptr_t) shared | (uintptr_t) residual | (uintptr_t) x_out | (uintptr_t) norm_weight) & 15u) ||
+        (o_stride & 3) || (shared_stride & 3))
+        return fail(E_INVALID, "combine: fp32 rows and strides must be 16-byte aligned");
     CombineArgs c;
     c.o = o;
     c.o_stride = o_stride;

@@ -18,7 +18,9 @@ enum : int {
     T_Q2_K = 10, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_Q8_K = 15
 };
 
-enum : int { ACT_Q8_1 = 0, ACT_Q8_K = 1 };
+// Activation formats: q8_1 blocks, q8_K blocks, or fp32 rows that the GEMV
+// quantizes to q8_1 itself (same codes and scales as the q8_1 quantizer).
+enum : int { ACT_Q8_1 = 0, ACT_Q8_K = 1, ACT_F32 = 2 };
 
 // Device stats buffer: [0] miss count, [1] resident-hit count,
 // [2 .. 2+MISS_CAP) miss log of (cache_id << 12 | expert) entries
@@ -120,6 +122,7 @@ struct GemvArgs {
     uint32_t act_row_bytes;       // bytes of one activation row
     uint32_t lds_span;            // LDS bytes per staged matrix span (up at 0, gate at lds_span)
     uint32_t lds_act;             // LDS offset of the staged activation row
+    uint32_t lds_q8;              // LDS offset of the in-kernel q8_1 copy of an fp32 activation row
     uint32_t lds_red;             // LDS offset of the 64-float reduction scratch
     uint32_t lds_total;           // dynamic LDS bytes per workgroup
 };
@@ -161,11 +164,11 @@ struct CombineArgs {
 };
 
 // Canonical order of the RMS sum of a row of k values (k % 256 == 0), shared by
-// the combine kernel, the persistent decode kernel and the CPU oracle: chunk j
-// holds values [256j, 256j+256); lane l of a 64-lane group accumulates
-// v = x[256j + 64p + l] for p = 0..3 as a = fmaf(v, v, a) starting from 0;
-// the 64 lane sums are tree-added (lane l += lane l+off, off = 32, 16, ..., 1);
-// chunk sums are added in ascending j starting from 0; s = 1 / sqrtf(sum/k + eps).
+// the combine kernel and the CPU oracle: chunk j holds values [256j, 256j+256);
+// lane l of a 64-lane group accumulates v = x[256j + 4l + i] for i = 0..3 as
+// a = fmaf(v, v, a) starting from 0; the 64 lane sums are tree-added (lane l +=
+// lane l+off, off = 32, 16, ..., 1); chunk sums are added in ascending j starting
+// from 0; s = 1 / sqrtf(sum/k + eps).
 constexpr int RMS_CHUNK = 256;
 
 }  // namespace mc

@@ -89,7 +89,8 @@ template <int T, int ACT>
 __device__ __forceinline__ void run_step(const GemvArgs &a, uint8_t *lds, bool shared, int tile) {
     constexpr TypeGeom G = type_geom(T);
     constexpr int UE = G.unit_elems, UB = G.unit_bytes;
-    constexpr int AUB = ACT == ACT_Q8_1 ? UE / 32 * 36 : 292;   // activation bytes per unit
+    constexpr int AQ = ACT == ACT_F32 ? ACT_Q8_1 : ACT;          // block format the dots read
+    constexpr int AUB = AQ == ACT_Q8_1 ? UE / 32 * 36 : 292;     // activation bytes per unit
     const int lane = threadIdx.x;
     const int K = a.ncols;
     const int nu = K / UE;                   // units per row (<= 64, checked on the host)
@@ -151,22 +152,27 @@ __device__ __forceinline__ void run_step(const GemvArgs &a, uint8_t *lds, bool s
     const int row_local = lane / nu, col = lane % nu;
     const bool active = row_local < nrows_here;
     const int unit = row_local * nu + col;
-    const uint8_t *aslice = lds + a.lds_act + alead + (u32) col * AUB;
+    // fp32 activations: the wave quantizes its staged row to q8_1 blocks in LDS
+    const uint8_t *arow = lds + a.lds_act + alead;
+    if constexpr (ACT == ACT_F32) arow = lds + a.lds_q8;
+    const uint8_t *aslice = arow + (u32) col * AUB;
     Act<UE> A;
     float pu = 0.0f, pg = 0.0f;
     if (wgate) {
         wait_loads_at_most(n_up);            // activation and gate span have landed
+        if constexpr (ACT == ACT_F32) quantize_row_lds((const float *) (lds + a.lds_act + alead), lds + a.lds_q8, K);
         if (active) {
-            load_act_lds<UE, ACT>(A, aslice);
-            pg = span_unit_dot<T, ACT>(lds + a.lds_span, span_lead(wgate, start), unit, A);
+            load_act_lds<UE, AQ>(A, aslice);
+            pg = span_unit_dot<T, AQ>(lds + a.lds_span, span_lead(wgate, start), unit, A);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        if (active) pu = span_unit_dot<T, ACT>(lds, span_lead(wup, start), unit, A);
+        if (active) pu = span_unit_dot<T, AQ>(lds, span_lead(wup, start), unit, A);
     } else {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if constexpr (ACT == ACT_F32) quantize_row_lds((const float *) (lds + a.lds_act + alead), lds + a.lds_q8, K);
         if (active) {
-            load_act_lds<UE, ACT>(A, aslice);
-            pu = span_unit_dot<T, ACT>(lds, span_lead(wup, start), unit, A);
+            load_act_lds<UE, AQ>(A, aslice);
+            pu = span_unit_dot<T, AQ>(lds, span_lead(wup, start), unit, A);
         }
     }
     // row sums across the nu lanes of each row (cross-lane adds, no LDS)
@@ -326,42 +332,53 @@ __global__ __launch_bounds__(64) void mc_quantize_q8_K_kernel(const QuantArgs a)
 }
 
 // MoE combine + RMSNorm + q8_1 quantization of the result, one 1024-thread
-// workgroup (16 waves) per token row.  Pass 1: wave w combines the 256-value
-// chunks w, w+16, ... into LDS (combine_chunk, mc_core.h), which also yields the
-// chunk's canonical RMS sum:
+// workgroup (16 waves) per token row; wave w handles the 256-value chunks w and
+// w + 16 of the row in registers (combine_chunk / quantize_chunk, mc_core.h):
 //   x = residual + shared + sum_j w[j] * o[j]   (j ascending, fmaf) -> x_out
-// Pass 2: s = 1 / sqrtf(sum of chunk sums (ascending) / k + eps) and
-//   y = q8_1((x * s) * norm_weight)   (rms_norm; y = q8_1(x) otherwise).
+//   s = 1 / sqrtf(sum of the canonical chunk sums (ascending) / k + eps)
+//   y = q8_1((x * s) * norm_weight)   (rms_norm; y = q8_1(x) otherwise)
 // This is the weighted sum ggml performs after MUL_MAT_ID (MUL by the router
 // weights, then ADDs), the RMS_NORM + MUL in front of the next MoE block and the
-// quantize_q8_1 of the next GEMV's input, in one launch.
+// quantize_q8_1 of the next GEMV's input, in one launch.  The norm weights are
+// loaded before the workgroup barrier, so the second phase does not wait on memory.
 constexpr int COMBINE_MAX_K = 8192;
 constexpr int COMBINE_THREADS = 1024;
+constexpr int COMBINE_WAVES = COMBINE_THREADS / WAVE;
+constexpr int COMBINE_CHUNKS_PER_WAVE = COMBINE_MAX_K / RMS_CHUNK / COMBINE_WAVES;
 
 __global__ __launch_bounds__(COMBINE_THREADS) void mc_combine_q8_1_kernel(const CombineArgs a) {
-    __shared__ float xs[COMBINE_MAX_K];
     __shared__ float chunk_sum[COMBINE_MAX_K / RMS_CHUNK];
-    __shared__ float scale;
     const int64_t t = blockIdx.x;
-    const int wave = threadIdx.x / WAVE;
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const int nchunk = (int) (a.k / RMS_CHUNK);
-    for (int j = wave; j < nchunk; j += COMBINE_THREADS / WAVE) {
-        const float cs = combine_chunk(a.o + t * a.n_used * a.o_stride, a.o_stride, a.w + t * a.n_used, a.n_used,
-                                       a.shared ? a.shared + t * a.shared_stride : nullptr,
-                                       a.residual ? a.residual + t * a.k : nullptr,
-                                       a.x_out ? a.x_out + t * a.k : nullptr, xs, j);
-        if (threadIdx.x % WAVE == 0) chunk_sum[j] = cs;
+    const bool norm = a.rms_norm != 0;
+    float xv[COMBINE_CHUNKS_PER_WAVE][4];
+    v4f nwv[COMBINE_CHUNKS_PER_WAVE];
+#pragma unroll
+    for (int ci = 0; ci < COMBINE_CHUNKS_PER_WAVE; ++ci) {
+        const int j = wave + COMBINE_WAVES * ci;
+        nwv[ci] = v4f{1.0f, 1.0f, 1.0f, 1.0f};
+        if (j < nchunk) {
+            if (norm && a.norm_weight) nwv[ci] = *(const v4f *) (a.norm_weight + j * RMS_CHUNK + 4 * lane);
+            const float cs = combine_chunk(a.o + t * a.n_used * a.o_stride, a.o_stride, a.w + t * a.n_used, a.n_used,
+                                           a.shared ? a.shared + t * a.shared_stride : nullptr,
+                                           a.residual ? a.residual + t * a.k : nullptr,
+                                           a.x_out ? a.x_out + t * a.k : nullptr, j, xv[ci]);
+            if (lane == 0) chunk_sum[j] = cs;
+        }
     }
-    __syncthreads();
-    if (a.rms_norm && threadIdx.x == 0) {
-        float ss = 0.0f;
+    float s = 1.0f;
+    if (norm) {
+        __syncthreads();
+        float ss = 0.0f;                     // every wave adds the chunk sums in the same order
         for (int j = 0; j < nchunk; ++j) ss += chunk_sum[j];
-        scale = 1.0f / sqrtf(ss / (float) a.k + a.eps);
+        s = 1.0f / sqrtf(ss / (float) a.k + a.eps);
     }
-    __syncthreads();
-    const float s = a.rms_norm ? scale : 1.0f;
-    for (int j = wave; j < nchunk; j += COMBINE_THREADS / WAVE)
-        quantize_chunk(xs, a.rms_norm != 0, s, a.norm_weight, a.y + t * a.y_stride, j);
+#pragma unroll
+    for (int ci = 0; ci < COMBINE_CHUNKS_PER_WAVE; ++ci) {
+        const int j = wave + COMBINE_WAVES * ci;
+        if (j < nchunk) quantize_chunk(xv[ci], norm, s, nwv[ci], a.y + t * a.y_stride, j);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -394,6 +411,7 @@ static hipError_t launch_ts(const GemvArgs &a, int ts, hipStream_t s) {
 template <int TW>
 static hipError_t launch_act(const GemvArgs &a, int ts, int act, hipStream_t s) {
     if (act == ACT_Q8_1) return launch_ts<TW, ACT_Q8_1>(a, ts, s);
+    if (act == ACT_F32) return launch_ts<TW, ACT_F32>(a, ts, s);
     if constexpr (type_geom(TW).kquant) {
         if (act == ACT_Q8_K) {
             // q8_K activations exist for K-quant shared experts only
@@ -425,8 +443,11 @@ int launch_gemv(GemvArgs a, int tw, int ts, int act, void *stream) {
     const TypeGeom g = type_geom(tw);
     const int nu = a.ncols / g.unit_elems;
     const uint32_t rb = (uint32_t) nu * (uint32_t) g.unit_bytes;
-    a.act_row_bytes = act == ACT_Q8_1 ? (uint32_t) (a.ncols / 32 * 36) : (uint32_t) (a.ncols / 256 * 292);
-    const uint32_t act_span = round_up_1k(a.act_row_bytes + 20u);
+    a.act_row_bytes = act == ACT_Q8_1 ? (uint32_t) (a.ncols / 32 * 36)
+                    : act == ACT_Q8_K ? (uint32_t) (a.ncols / 256 * 292) : (uint32_t) a.ncols * 4u;
+    // fp32 rows also need room for their q8_1 copy
+    const uint32_t q8_bytes = act == ACT_F32 ? ((uint32_t) (a.ncols / 32 * 36) + 15u) & ~15u : 0u;
+    const uint32_t act_span = round_up_1k(a.act_row_bytes + 20u) + q8_bytes;
     if (ts == 0 || !a.sh_up) ts = 0;
     const int nspan = (a.has_gate || (ts != 0 && a.sh_gate)) ? 2 : 1;
     a.rps = fit_rows_per_step(nu, rb, nspan, act_span);
@@ -446,6 +467,7 @@ int launch_gemv(GemvArgs a, int tw, int ts, int act, void *stream) {
     }
     a.lds_span = span;
     a.lds_act = (uint32_t) nspan * span;
+    a.lds_q8 = a.lds_act + act_span - q8_bytes;
     a.lds_red = a.lds_act + act_span;
     a.lds_total = a.lds_red + 256u;
     a.rec = (a.stats || a.stamps || a.stamps_gate) ? 1 : 0;

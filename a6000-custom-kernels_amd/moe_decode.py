@@ -3,10 +3,10 @@
 Per layer, for one token (the op sequence of a ggml MoE FFN block):
   1. gate/up MUL_MAT_ID over the routed experts, fused SwiGLU, with the shared
      expert's gate/up in the same launch             -> h[0..n_used)   and h[n_used]
-  2. q8_1 quantization of the n_used+1 GLU rows    -> hq
-  3. down MUL_MAT_ID (one activation row per slot), shared expert's down in the
-     same launch                                    -> o[0..n_used) and o_sh
-  4. combine x' = x + o_sh + sum_j w_j o_j, fused with the next block's
+  2. down MUL_MAT_ID (one activation row per slot), shared expert's down in the
+     same launch, reading the fp32 GLU rows and quantizing them to q8_1 inside
+     the GEMV                                       -> o[0..n_used) and o_sh
+  3. combine x' = x + o_sh + sum_j w_j o_j, fused with the next block's
      ffn_norm (RMSNorm times its norm weight) and the q8_1 quantization of the
      normalized row for the next layer's gate/up launch.
 Every launch goes through the C ABI (include/ggml_hip_moe_cache.h); one token is
@@ -25,7 +25,7 @@ import math
 
 import numpy as np
 
-from . import (ACT_Q8_1, BLOCK, GLU_SWIGLU, KQUANTS, Q2_K, Q3_K, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0, check,
+from . import (ACT_F32, ACT_Q8_1, BLOCK, GLU_SWIGLU, KQUANTS, Q2_K, Q3_K, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0, check,
                lib, make_fusion, make_tensor, row_bytes)
 
 # byte offsets of the fp16 block-scale fields per type, and the value written there
@@ -87,7 +87,6 @@ class MoeDecodeModel:
         self.x_next = torch.zeros((1, hidden), dtype=f32, device=device)
         self.y = torch.zeros((1, hidden // 32 * 36), dtype=u8, device=device)
         self.h = torch.zeros((n_used + 1, ffn), dtype=f32, device=device)   # row n_used: shared expert
-        self.hq = torch.zeros((n_used + 1, ffn // 32 * 36), dtype=u8, device=device)
         self.o = torch.zeros((n_used, hidden), dtype=f32, device=device)
         self.o_sh = torch.zeros((1, hidden), dtype=f32, device=device)
         self.ids = torch.zeros((n_layers, 1, n_used), dtype=i32, device=device)
@@ -98,7 +97,7 @@ class MoeDecodeModel:
             ly.f_gu = make_fusion(gate=ly.gate, glu_op=GLU_SWIGLU, shared_up=ly.sh_up, shared_gate=ly.sh_gate,
                                   shared_dst=self.h[n_used:], shared_type=sh_type)
             ly.f_dn = make_fusion(shared_up=ly.sh_down, shared_dst=self.o_sh, shared_type=sh_type,
-                                  shared_src1=self.hq[n_used:], shared_stride_col_y=ffn // 32)
+                                  shared_src1=self.h[n_used:], shared_stride_col_y=ffn)
         self.graph = None
 
     # bytes one token reads by definition (unique expert matrices + shared + activations + outputs)
@@ -107,7 +106,7 @@ class MoeDecodeModel:
         eb_gu = row_bytes(self.wtype, H) * F
         eb_dn = row_bytes(self.wtype, F) * H
         sh = row_bytes(self.sh_type, H) * F * 2 + row_bytes(self.sh_type, F) * H
-        act = H // 32 * 36 + (U + 1) * F // 32 * 36
+        act = H // 32 * 36 + (U + 1) * F * 4          # q8_1 input row, fp32 GLU rows
         out = (U + 1) * F * 4 + (U + 1) * H * 4
         norm = H * 4
         return self.L * (U * (2 * eb_gu + eb_dn) + sh + act + out + norm)
@@ -119,7 +118,7 @@ class MoeDecodeModel:
 
     def down_bytes(self):
         H, F, U = self.H, self.F, self.U
-        return U * row_bytes(self.wtype, F) * H + row_bytes(self.sh_type, F) * H + (U + 1) * F // 32 * 36 + (U + 1) * H * 4
+        return U * row_bytes(self.wtype, F) * H + row_bytes(self.sh_type, F) * H + (U + 1) * F * 4 + (U + 1) * H * 4
 
     def _stream(self):
         return C.c_void_p(self.torch.cuda.current_stream().cuda_stream)
@@ -136,16 +135,15 @@ class MoeDecodeModel:
         ly = self.layers[l]
         s = s or self._stream()
         H, F, U = self.H, self.F, self.U
-        check(lib().ggml_hip_moe_mul_mat_vec_ex(0, ACT_Q8_1, C.byref(ly.t_down), None, C.byref(ly.f_dn),
-                                                self.hq.data_ptr(), self.ids[l].data_ptr(), self.o.data_ptr(),
-                                                F, H, self.E, 1, U, U, (U + 1) * F // 32, U * H, F // 32, H, U, s),
+        check(lib().ggml_hip_moe_mul_mat_vec_ex(0, ACT_F32, C.byref(ly.t_down), None, C.byref(ly.f_dn),
+                                                self.h.data_ptr(), self.ids[l].data_ptr(), self.o.data_ptr(),
+                                                F, H, self.E, 1, U, U, (U + 1) * F, U * H, F, H, U, s),
               "down")
 
     def launch_layer(self, l, s=None):
         s = s or self._stream()
         H, F, U = self.H, self.F, self.U
         self.launch_gate_up(l, s)
-        check(lib().ggml_hip_quantize_q8_1(self.h.data_ptr(), self.hq.data_ptr(), F, U + 1, F, F // 32, s), "quantize h")
         self.launch_down(l, s)
         src, dst = (self.x, self.x_next) if l % 2 == 0 else (self.x_next, self.x)
         nxt = self.norm[(l + 1) % self.L]        # the next block's ffn_norm (layer 0's for the next token)

@@ -64,7 +64,9 @@ enum {
 /* Activation formats accepted by the GEMV (src1 after quantization). */
 enum {
     GGML_HIP_MOE_ACT_Q8_1 = 0, /* ggml-CUDA q8_1 blocks (36 B / 32 values): the reference's src1_q8_1 */
-    GGML_HIP_MOE_ACT_Q8_K = 1  /* ggml-CPU q8_K blocks (292 B / 256 values), K-quant weights only */
+    GGML_HIP_MOE_ACT_Q8_K = 1, /* ggml-CPU q8_K blocks (292 B / 256 values), K-quant weights only */
+    GGML_HIP_MOE_ACT_F32  = 2  /* fp32 rows, quantized to q8_1 inside the GEMV with the codes and
+                                  scales ggml_hip_quantize_q8_1 produces (fuses that launch away) */
 };
 
 /* POD mirror of the ggml_tensor fields the path reads
@@ -167,7 +169,8 @@ int ggml_hip_mul_mat_vec_q_moe(
 /* Both GEMV entry points with an explicit activation format
  * (GGML_HIP_MOE_ACT_*).  use_cache = 1 takes the cache path (src0 must satisfy
  * ggml_hip_moe_cache_wants), 0 the device-resident path.  With
- * GGML_HIP_MOE_ACT_Q8_K the activation strides count q8_K blocks (256 values). */
+ * GGML_HIP_MOE_ACT_Q8_K the activation strides count q8_K blocks (256 values), with
+ * GGML_HIP_MOE_ACT_F32 they count floats (src1 and shared_src1 are fp32 rows). */
 int ggml_hip_moe_mul_mat_vec_ex(
         int use_cache, int act_format,
         const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *gate_host,
@@ -204,12 +207,14 @@ int ggml_hip_quantize_q8_0_as_q8_1(const float *x, void *y, int64_t k, int64_t n
  * The mean of squares is summed in a fixed order (256-value chunks, see mc_internal.h), so results are
  * deterministic.  o: [n_tok][n_used][o_stride] floats (n_used <= 16); w: [n_tok][n_used]; shared:
  * [n_tok][shared_stride] or NULL; residual: [n_tok][k] or NULL; x_out: [n_tok][k] or NULL; y_q8_1: n_tok
- * rows, y_stride blocks apart; norm_weight: [k] or NULL; k % 256 == 0, k <= 8192.  No reference
- * counterpart (ggml runs these as separate ops). */
+ * rows, y_stride blocks apart; norm_weight: [k] or NULL; k % 256 == 0, k <= 8192; fp32 pointers
+ * 16-byte aligned, o_stride and shared_stride multiples of 4.  No reference counterpart (ggml runs
+ * these as separate ops). */
 int ggml_hip_moe_combine_q8_1(const float *o, int64_t o_stride, const float *w, int32_t n_used,
                               const float *shared, int64_t shared_stride, const float *residual,
                               float *x_out, void *y_q8_1, int64_t y_stride, int64_t k, int64_t n_tok,
                               int32_t rms_norm, const float *norm_weight, float eps, void *stream);
+
 
 /* ---------------------------------------------------------------------
  * Configuration, introspection and teardown (the reference reads env vars

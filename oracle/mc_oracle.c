@@ -916,9 +916,9 @@ int or_cpu_mul_mat_id_f32(int type, int64_t ne00, int64_t ne01, int32_t n_as,
     return 0;
 }
 
-/* RMS sum of a row in the canonical order of the GPU kernels: 256-value chunks;
- * in chunk j, partial l (0..63) accumulates x[256j + 64p + l]^2 (p = 0..3) with
- * fmaf from 0; the 64 partials are tree-added (l += l + off, off = 32 .. 1);
+/* RMS sum of a row in the canonical order of the GPU combine kernel: 256-value
+ * chunks; in chunk j, partial l (0..63) accumulates x[256j + 4l + i]^2 (i = 0..3)
+ * with fmaf from 0; the 64 partials are tree-added (l += l + off, off = 32 .. 1);
  * chunk sums are added in ascending j from 0. */
 float or_rms_sum(const float *x, int64_t k) {
     float total = 0.0f;
@@ -926,8 +926,8 @@ float or_rms_sum(const float *x, int64_t k) {
         float part[64];
         for (int l = 0; l < 64; ++l) {
             float a = 0.0f;
-            for (int p = 0; p < 4; ++p) {
-                const float v = x[256 * j + 64 * p + l];
+            for (int i = 0; i < 4; ++i) {
+                const float v = x[256 * j + 4 * l + i];
                 a = fmaf(v, v, a);
             }
             part[l] = a;

@@ -41,10 +41,8 @@ def test_decode_layer_stagewise(torch_gpu, mc, O, small_model):
     assert O.rel_l2(h[:U], want_h[0]) <= 1e-5
     assert O.rel_l2(h[U], want_hs[0]) <= 1e-5
 
-    mc.quantize_q8_1(m.h, out=m.hq)
-    torch.cuda.synchronize()
-    hq = m.hq.cpu().numpy()
-    assert np.array_equal(hq, np.stack([O.quantize_q8_1(r) for r in h]))
+    # the down GEMV quantizes the fp32 GLU rows itself: its input is q8_1 of the GPU's h bytes
+    hq = np.stack([O.quantize_q8_1(r) for r in h])
 
     m.launch_down(0)
     torch.cuda.synchronize()
@@ -57,6 +55,8 @@ def test_decode_layer_stagewise(torch_gpu, mc, O, small_model):
 
     nw = m.norm[1]
     for norm, weight in ((False, None), (True, None), (True, nw)):
+        m.x_next.zero_()
+        m.y.zero_()
         mc.combine_q8_1(m.o.view(1, U, H), m.w[0], shared=m.o_sh, residual=m.x, x_out=m.x_next, y=m.y,
                         rms_norm=norm, norm_weight=weight, eps=1e-6)
         torch.cuda.synchronize()

@@ -177,3 +177,56 @@ def test_gemv_down_projection_channels(torch_gpu, mc, O):
     err = O.rel_l2(got, want)
     _note(f"down rel_l2={err:.3e}")
     assert err <= 1e-5
+
+
+@pytest.mark.parametrize("wtype,shtype,K,gated", [(10, 12, 768, False), (2, 10, 1024, True), (12, 12, 4096, True),
+                                                   (14, 11, 512, False), (6, 8, 2048, False)])
+def test_gemv_f32_activations_equal_q8_1_path(torch_gpu, mc, O, wtype, shtype, K, gated):
+    """fp32 activation rows quantized inside the GEMV give bit-identical outputs to the
+    q8_1 quantizer followed by the q8_1 GEMV (routed slots with one row each, plus the
+    shared expert reading its own row)."""
+    torch = torch_gpu
+    R, n_exp, n_used, n_tok = 70, 12, 4, 2
+    _note(f"gemv f32 act type={wtype} shared={shtype} K={K} gated={gated}")
+    up = H.weights(wtype, n_exp, R, K, seed=1001 + wtype)
+    gate = H.weights(wtype, n_exp, R, K, seed=1002 + wtype) if gated else None
+    sh_up = H.weights(shtype, 1, R, K, seed=1003)[0]
+    x = H.activations(n_tok * (n_used + 1), K, seed=1004 + K).reshape(n_tok, n_used + 1, K)
+    x[0, 1] = 0.0                                         # an all-zero row: d = 0, codes 0
+    ids = H.routing(n_tok, n_used, n_exp, seed=1005)
+    xd = _dev(torch, x)
+    ids_d = _dev(torch, ids)
+    yq = mc.quantize_q8_1(xd.view(-1, K)).view(n_tok, n_used + 1, -1)
+    sh_up_d = _dev(torch, sh_up)
+    outs = []
+    for act, y, sh_row, stride in ((mc.ACT_Q8_1, yq, yq[:, n_used], (n_used + 1) * K // 32),
+                                   (mc.ACT_F32, xd, xd[:, n_used], (n_used + 1) * K)):
+        sh_dst = torch.zeros((n_tok, R), dtype=torch.float32, device="cuda")
+        dst = torch.zeros((n_tok, n_used, R), dtype=torch.float32, device="cuda")
+        f = mc.make_fusion(glu_op=2, shared_up=sh_up_d, shared_dst=sh_dst, shared_type=shtype,
+                           shared_src1=sh_row, shared_stride_col_y=stride)
+        keep = [f]
+        if gated:
+            gd = _dev(torch, gate)
+            keep.append(gd)
+            f.gate = gd.data_ptr()
+        wd = _dev(torch, up)
+        blk = 32 if act == mc.ACT_Q8_1 else 1
+        src0 = mc.make_tensor(wtype, K, R, n_exp, wd.data_ptr(), keep=keep)
+        import ctypes as C
+        rc = mc.lib().ggml_hip_moe_mul_mat_vec_ex(0, act, C.byref(src0), None, C.byref(f), y.data_ptr(),
+                                                   ids_d.data_ptr(), dst.data_ptr(), K, R, n_exp, n_tok,
+                                                   n_used + 1, n_used, (n_used + 1) * K // blk, n_used * R, K // blk, R,
+                                                   n_used, None)
+        mc.check(rc, "mul_mat_vec_ex")
+        torch.cuda.synchronize()
+        outs.append((dst.cpu().numpy(), sh_dst.cpu().numpy()))
+    assert np.isfinite(outs[0][0]).all() and np.isfinite(outs[0][1]).all()
+    assert np.array_equal(outs[0][0], outs[1][0])
+    assert np.array_equal(outs[0][1], outs[1][1])
+    # and the q8_1 path itself against the oracle on the same bytes
+    yq_np = yq.cpu().numpy()
+    want, want_sh = O.mul_mat_id(wtype=wtype, K=K, R=R, n_as=n_exp, src0=up, gate=gate, ids=ids, act=yq_np[:, :n_used],
+                                 act_kind=O.ACT_Q8_1, nchannels_y=n_used, glu_op=2, sh_type=shtype, sh_up=sh_up,
+                                 sh_act=yq_np[:, n_used])
+    assert O.rel_l2(outs[0][0], want) <= 1e-5 and O.rel_l2(outs[0][1], want_sh) <= 1e-5
