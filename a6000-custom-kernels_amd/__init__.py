@@ -91,6 +91,9 @@ SIGNATURES = [
     ("ggml_hip_quantize_q8_0_as_q8_1", C.c_int, [_VP, _VP, _I64, _I64, _I64, _I64, _VP]),
     ("ggml_hip_moe_combine_q8_1", C.c_int,
      [_VP, _I64, _VP, _I32, _VP, _I64, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP, C.c_float, _VP]),
+    ("ggml_hip_moe_mul_mat_q_workspace_bytes", C.c_int64, [_I64, _I64, _I64]),
+    ("ggml_hip_moe_mul_mat_q", C.c_int,
+     [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _I64, _VP]),
     ("ggml_hip_moe_cache_configure", C.c_int, [C.POINTER(Config)]),
     ("ggml_hip_moe_cache_get_config", C.c_int, [C.POINTER(Config)]),
     ("ggml_hip_moe_cache_num_entries", C.c_int, []),
@@ -250,6 +253,32 @@ def mul_mat_vec(*, wtype, weights, ids, y, dst, K, R, n_experts, use_cache=False
         K, R, n_experts, n_tok, nchannels_y, n_used,
         nchannels_y * act_row, n_used * R, act_row, R, ids.stride(0), _stream(stream))
     check(rc, "mul_mat_vec")
+    return dst
+
+
+def mul_mat_q(*, wtype, weights, ids, y, dst, K, R, n_experts, gate=None, glu_op=GLU_SWIGLU, glu_limit=0.0,
+              nchannels_y=1, workspace=None, stream=None):
+    """Prefill-shaped MUL_MAT_ID through ggml_hip_moe_mul_mat_q (expert-grouped int8 MFMA).
+
+    weights/gate: device uint8 [n_experts, R, row_bytes] (Q4_K or Q5_K); ids: int32 [n_tok, n_used];
+    y: q8_K rows [n_tok, nchannels_y, K/256*292] (device, 256-byte aligned); dst: float32 [n_tok, n_used, R].
+    Returns dst.
+    """
+    torch = _torch()
+    n_tok, n_used = ids.shape
+    _require_gpu(weights, ids, y, dst, gate)
+    keep = []
+    src0 = make_tensor(wtype, K, R, n_experts, weights.data_ptr(), keep=keep)
+    f = make_fusion(gate=gate, glu_op=glu_op, glu_limit=glu_limit) if gate is not None else None
+    nbytes = int(lib().ggml_hip_moe_mul_mat_q_workspace_bytes(K, n_experts, n_tok * n_used))
+    if workspace is None or workspace.numel() < nbytes:
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=dst.device)
+    nb = K // 256
+    rc = lib().ggml_hip_moe_mul_mat_q(C.byref(src0), C.byref(f) if f is not None else None, y.data_ptr(),
+                                      ids.data_ptr(), dst.data_ptr(), K, R, n_experts, n_tok, nchannels_y, n_used,
+                                      nchannels_y * nb, n_used * R, nb, R, ids.stride(0), workspace.data_ptr(),
+                                      workspace.numel(), _stream(stream))
+    check(rc, "mul_mat_q")
     return dst
 
 

@@ -34,6 +34,7 @@ struct Device {
     virtual int launch_gemv(const GemvArgs &a, int tw, int ts, int act, void *stream) = 0;
     virtual int launch_quantize(int kind, const QuantArgs &q, void *stream) = 0;
     virtual int launch_combine(const CombineArgs &c, void *stream) = 0;
+    virtual int launch_mmq(const MmqArgs &m, int type, void *stream) = 0;
     virtual const char *error_string(int code) = 0;
 };
 

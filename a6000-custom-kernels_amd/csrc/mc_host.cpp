@@ -782,6 +782,69 @@ int ggml_hip_moe_combine_q8_1(const float *o, int64_t o_stride, const float *w, 
     return 0;
 }
 
+int64_t ggml_hip_moe_mul_mat_q_workspace_bytes(int64_t ne00, int64_t ne02, int64_t n_pairs) {
+    if (ne00 <= 0 || ne00 % 256 || ne02 <= 0 || n_pairs < 0) return 0;
+    MmqArgs a = {};
+    a.ncols = (int32_t) ne00;
+    a.n_experts = (int32_t) ne02;
+    mmq_layout(a, n_pairs);
+    return (int64_t) a.ws_total;
+}
+
+int ggml_hip_moe_mul_mat_q(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_fusion *fusion, const void *src1_q8_K,
+                           const int32_t *ids_d, float *dst_d, int64_t ne00, int64_t ne01, int64_t ne02,
+                           int64_t ncols_dst, int64_t nchannels_y, int64_t nchannels_dst, int64_t stride_col_y,
+                           int64_t stride_col_dst, int64_t stride_channel_y, int64_t stride_channel_dst,
+                           int64_t ids_stride, void *workspace, int64_t workspace_bytes, void *stream) {
+    if (!src0 || !src0->data || !src1_q8_K || !ids_d || !dst_d || !workspace)
+        return fail(E_INVALID, "mul_mat_q: null argument");
+    const int tw = src0->type;
+    if (tw != T_Q4_K && tw != T_Q5_K) return fail(E_UNSUPPORTED, "mul_mat_q: expert type %d is not supported", tw);
+    if (ne00 <= 0 || ne00 % 256 || ne01 <= 0 || ne02 <= 0 || ncols_dst <= 0 || nchannels_dst <= 0 || nchannels_y <= 0)
+        return fail(E_INVALID, "mul_mat_q: bad shape");
+    if (ne02 > MMQ_MAX_EXPERTS) return fail(E_UNSUPPORTED, "mul_mat_q: more than %d experts", MMQ_MAX_EXPERTS);
+    if (src0->ne[0] != ne00 || src0->ne[1] != ne01 || src0->ne[2] != ne02 || !is_contiguous(src0))
+        return fail(E_INVALID, "mul_mat_q: src0 shape/strides do not match the call");
+    if (ids_stride < nchannels_dst) return fail(E_INVALID, "mul_mat_q: ids_stride < nchannels_dst");
+    if (ncols_dst * nchannels_dst > INT32_MAX) return fail(E_INVALID, "mul_mat_q: too many pairs");
+    if (fusion && (fusion->x_bias || fusion->gate_bias || fusion->x_scale || fusion->gate_scale || fusion->shared_up))
+        return fail(E_UNSUPPORTED, "mul_mat_q: only the gate/GLU fusion is supported");
+    const uint64_t eb = (uint64_t) src0->nb[2];
+    if (eb > 0xFFFFFFF0ull) return fail(E_UNSUPPORTED, "mul_mat_q: expert matrix larger than 4 GiB");
+    if (((uintptr_t) src0->data | eb | (uintptr_t) (fusion ? fusion->gate : nullptr)) & 15u)
+        return fail(E_UNSUPPORTED, "mul_mat_q: expert weights must be 16-byte aligned");
+    if (((uintptr_t) src1_q8_K | (uintptr_t) workspace) & 255u)
+        return fail(E_INVALID, "mul_mat_q: activations and workspace must be 256-byte aligned");
+    MmqArgs a = {};
+    a.w = (const uint8_t *) src0->data;
+    a.w_gate = fusion ? (const uint8_t *) fusion->gate : nullptr;
+    a.expert_bytes = eb;
+    a.y = (const uint8_t *) src1_q8_K;
+    a.stride_col_y = stride_col_y * 292;
+    a.stride_channel_y = stride_channel_y * 292;
+    a.nchannels_y = (int32_t) nchannels_y;
+    a.ids = ids_d;
+    a.ids_stride = ids_stride;
+    a.dst = dst_d;
+    a.stride_col_dst = stride_col_dst;
+    a.stride_channel_dst = stride_channel_dst;
+    a.ncols = (int32_t) ne00;
+    a.nrows = (int32_t) ne01;
+    a.n_experts = (int32_t) ne02;
+    a.n_used = (int32_t) nchannels_dst;
+    a.n_tok = (int32_t) ncols_dst;
+    a.glu_op = fusion ? fusion->glu_op : 2;
+    a.glu_limit = fusion ? fusion->glu_limit : 0.0f;
+    a.ws = (uint8_t *) workspace;
+    mmq_layout(a, ncols_dst * nchannels_dst);
+    if ((uint64_t) workspace_bytes < a.ws_total)
+        return fail(E_INVALID, "mul_mat_q: workspace of %lld bytes, %llu needed", (long long) workspace_bytes,
+                    (unsigned long long) a.ws_total);
+    const int rc = dev()->launch_mmq(a, tw, stream);
+    if (rc) return dev_err(rc, "mul_mat_q launch");
+    return 0;
+}
+
 int ggml_hip_moe_cache_configure(const ggml_hip_moe_config *cfg) {
     if (!cfg) return fail(E_INVALID, "configure: null config");
     std::lock_guard<std::mutex> lock(g_mutex);

@@ -171,6 +171,55 @@ struct CombineArgs {
 // from 0; s = 1 / sqrtf(sum/k + eps).
 constexpr int RMS_CHUNK = 256;
 
+// ---------------------------------------------------------------------------
+// prefill-shaped MUL_MAT_ID (mc_mmq.hip)
+// ---------------------------------------------------------------------------
+
+constexpr int MMQ_COLS = 16;              // (token, slot) pairs per column block: the MFMA M dimension
+constexpr int MMQ_WAVES = 4;              // waves per GEMM workgroup, 16 weight rows each
+constexpr int MMQ_ROWS = 16 * MMQ_WAVES;  // weight rows per GEMM workgroup
+constexpr int MMQ_MAX_BLOCKS = 4;         // column blocks multiplied per pass over an expert's weights
+constexpr int MMQ_MAX_EXPERTS = 4096;
+constexpr int MMQ_REC_BYTES = 4416;       // activation record of one (super-block, column block)
+
+struct MmqArgs {
+    const uint8_t *w;             // expert weights (device), expert e at w + e * expert_bytes
+    const uint8_t *w_gate;        // gate weights of the same shape, or null (then no GLU)
+    uint64_t expert_bytes;
+    const uint8_t *y;             // q8_K activation rows
+    int64_t stride_col_y;         // bytes between tokens
+    int64_t stride_channel_y;     // bytes between channels
+    int32_t nchannels_y;
+    const int32_t *ids;           // [n_tok][ids_stride]
+    int64_t ids_stride;
+    float *dst;                   // dst[t * stride_col_dst + c * stride_channel_dst + row]
+    int64_t stride_col_dst;
+    int64_t stride_channel_dst;
+    int32_t ncols;                // K (multiple of 256)
+    int32_t nrows;                // rows per expert
+    int32_t n_experts;
+    int32_t n_used;
+    int32_t n_tok;
+    int32_t glu_op;
+    float glu_limit;
+    int32_t max_blocks;           // capacity of the column-block table
+    uint8_t *ws;                  // workspace base and the byte offsets of its sections
+    uint64_t ws_offsets, ws_blk_off, ws_list, ws_blk_tab, ws_packed, ws_total;
+};
+
+// Workspace sections for n_experts experts, n_pairs pairs and K values per row.
+inline void mmq_layout(MmqArgs &a, int64_t n_pairs) {
+    const auto up = [](uint64_t b) { return (b + 255u) & ~(uint64_t) 255u; };
+    a.max_blocks = (int32_t) (a.n_experts + (n_pairs + MMQ_COLS - 1) / MMQ_COLS);
+    uint64_t o = 0;
+    a.ws_offsets = o; o = up(o + 4u * (uint64_t) (a.n_experts + 1));
+    a.ws_blk_off = o; o = up(o + 4u * (uint64_t) (a.n_experts + 1));
+    a.ws_list = o; o = up(o + 4u * (uint64_t) n_pairs);
+    a.ws_blk_tab = o; o = up(o + 16u * (uint64_t) a.max_blocks);
+    a.ws_packed = o; o = up(o + (uint64_t) MMQ_REC_BYTES * (uint64_t) a.max_blocks * (uint64_t) (a.ncols / 256));
+    a.ws_total = o + 1024u;       // slack for the last DMA round
+}
+
 }  // namespace mc
 
 #endif

@@ -1,0 +1,392 @@
+// mc_mmq.hip -- prefill-shaped MUL_MAT_ID on gfx950: the (token, slot) pairs are
+// grouped by expert and each expert's weights are multiplied against all of its
+// pairs at once with int8 MFMA (v_mfma_i32_16x16x32_i8).
+//
+// Replaces the many-token MUL_MAT_ID path the reference leaves to upstream
+// ggml (MMQ; results/final.patch:45-48 only routes batch-1 decode to the
+// pointer-table GEMV).  Activations are q8_K rows (one scale per 256 values,
+// exact 16-value sums), the ggml-CPU vec_dot_type of the K-quants
+// (patches/trace-hook/ggml-cpu.c:308-340): the eight 32-value sub-block
+// products of a super-block then accumulate exactly in int32 (sub-block scale
+// times the MFMA result), with one float update per super-block.
+//
+// Three launches:
+//   1. mc_mmq_group_kernel  (one workgroup): pair counts per expert, offsets,
+//      the pair list grouped by expert and a table of 16-pair column blocks.
+//   2. mc_mmq_pack_kernel: per (super-block, column block) one record holding the
+//      MFMA A fragments of the 16 pairs' activation codes, their q8_K scales and
+//      32-value sums (zeros for empty columns).
+//   3. mc_mmq_gemm_kernel<T, GATE>: one workgroup per (64 weight rows, expert);
+//      per super-block it DMAs the 64 rows' weight blocks and the records of up
+//      to MMQ_MAX_BLOCKS column blocks into LDS (double-buffered), each wave
+//      multiplies 16 weight rows against them, and the epilogue applies the GLU
+//      (when a gate matrix is fused) and scatters to dst[token][slot][row].
+// The position of a pair inside its expert's group depends on atomic order, but
+// every pair's result is computed by the same integer MFMA sums and the same
+// float operations wherever it lands, so the output does not depend on it.
+#include <hip/hip_runtime.h>
+
+#include "mc_core.h"
+#include "mc_internal.h"
+
+namespace mc {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// 1. grouping
+// ---------------------------------------------------------------------------
+
+constexpr int MMQ_GROUP_THREADS = 1024;
+
+// Exclusive prefix sum over a 1024-thread workgroup (each thread one value).
+__device__ __forceinline__ int block_exclusive_scan(int v, int *lds_waves, int &total) {
+    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    int incl = v;
+#pragma unroll
+    for (int off = 1; off < WAVE; off <<= 1) {
+        const int o = __shfl_up(incl, off, WAVE);
+        if (lane >= off) incl += o;
+    }
+    if (lane == WAVE - 1) lds_waves[wave] = incl;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int run = 0;
+        for (int i = 0; i < MMQ_GROUP_THREADS / WAVE; ++i) {
+            const int t = lds_waves[i];
+            lds_waves[i] = run;
+            run += t;
+        }
+        lds_waves[MMQ_GROUP_THREADS / WAVE] = run;
+    }
+    __syncthreads();
+    total = lds_waves[MMQ_GROUP_THREADS / WAVE];
+    const int r = lds_waves[wave] + incl - v;
+    __syncthreads();
+    return r;
+}
+
+__global__ __launch_bounds__(MMQ_GROUP_THREADS) void mc_mmq_group_kernel(const MmqArgs a) {
+    __shared__ int cnt[MMQ_MAX_EXPERTS];
+    __shared__ int fill[MMQ_MAX_EXPERTS];
+    __shared__ int scan_tmp[MMQ_GROUP_THREADS / WAVE + 1];
+    int *offsets = (int *) (a.ws + a.ws_offsets);      // [E + 1]
+    int *blk_off = (int *) (a.ws + a.ws_blk_off);      // [E + 1]
+    int *list = (int *) (a.ws + a.ws_list);            // [n_pairs]
+    int *blk_tab = (int *) (a.ws + a.ws_blk_tab);      // [max_blocks][4]: expert, first position, pairs
+    const int E = a.n_experts, n_pairs = a.n_tok * a.n_used;
+    for (int e = threadIdx.x; e < E; e += MMQ_GROUP_THREADS) {
+        cnt[e] = 0;
+        fill[e] = 0;
+    }
+    __syncthreads();
+    for (int p = threadIdx.x; p < n_pairs; p += MMQ_GROUP_THREADS) {
+        const int t = p / a.n_used, c = p % a.n_used;
+        const int e = a.ids[c + (int64_t) t * a.ids_stride];
+        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    // offsets and column-block offsets: experts in ascending order, 4 per thread
+    constexpr int PER = MMQ_MAX_EXPERTS / MMQ_GROUP_THREADS;
+    int c4[PER], b4[PER], csum = 0, bsum = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int e = threadIdx.x * PER + i;
+        c4[i] = e < E ? cnt[e] : 0;
+        b4[i] = (c4[i] + MMQ_COLS - 1) / MMQ_COLS;
+        csum += c4[i];
+        bsum += b4[i];
+    }
+    int ctot, btot;
+    int crun = block_exclusive_scan(csum, scan_tmp, ctot);
+    int brun = block_exclusive_scan(bsum, scan_tmp, btot);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int e = threadIdx.x * PER + i;
+        if (e < E) {
+            offsets[e] = crun;
+            blk_off[e] = brun;
+            for (int b = 0; b < b4[i]; ++b) {
+                int *row = blk_tab + 4 * (brun + b);
+                row[0] = e;
+                row[1] = crun + MMQ_COLS * b;
+                row[2] = min(MMQ_COLS, c4[i] - MMQ_COLS * b);
+                row[3] = 0;
+            }
+            fill[e] = crun;
+        }
+        crun += c4[i];
+        brun += b4[i];
+    }
+    if (threadIdx.x == 0) {
+        offsets[E] = ctot;
+        blk_off[E] = btot;
+    }
+    __syncthreads();
+    for (int p = threadIdx.x; p < n_pairs; p += MMQ_GROUP_THREADS) {
+        const int t = p / a.n_used, c = p % a.n_used;
+        const int e = a.ids[c + (int64_t) t * a.ids_stride];
+        if (e >= 0 && e < E) list[atomicAdd(&fill[e], 1)] = p;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 2. activation records
+// ---------------------------------------------------------------------------
+
+// Record of one (super-block s, column block b), at ws_packed + (s * max_blocks + b) * MMQ_REC_BYTES:
+//   [0, 4096)     A fragments: sub-block sb, lane l -> 8 codes of pair l % 16, values 32 sb + 8 (l / 16) .. +7
+//   [4096, 4160)  d8[16]: the pairs' q8_K scales
+//   [4160, 4416)  S[16][8] int16: the pairs' 32-value code sums per sub-block
+constexpr int MMQ_REC_FRAG = 0, MMQ_REC_D8 = 4096, MMQ_REC_SUM = 4160;
+
+__global__ __launch_bounds__(256) void mc_mmq_pack_kernel(const MmqArgs a) {
+    const int n_sb = a.ncols / 256;
+    const int64_t gid = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;   // (block, column, super-block)
+    const int s = (int) (gid % n_sb);
+    const int64_t bc = gid / n_sb;
+    const int col = (int) (bc % MMQ_COLS);
+    const int b = (int) (bc / MMQ_COLS);
+    const int *blk_off = (const int *) (a.ws + a.ws_blk_off);
+    if (b >= a.max_blocks || b >= blk_off[a.n_experts]) return;
+    const int *row = (const int *) (a.ws + a.ws_blk_tab) + 4 * b;
+    uint8_t *rec = a.ws + a.ws_packed + ((int64_t) s * a.max_blocks + b) * MMQ_REC_BYTES;
+    uint64_t *frag = (uint64_t *) (rec + MMQ_REC_FRAG);
+    float *d8 = (float *) (rec + MMQ_REC_D8);
+    int16_t *sums = (int16_t *) (rec + MMQ_REC_SUM) + 8 * col;
+    if (col >= row[2]) {                      // empty column: zero codes, scale and sums
+#pragma unroll
+        for (int sb = 0; sb < 8; ++sb)
+#pragma unroll
+            for (int kq = 0; kq < 4; ++kq) frag[sb * 64 + col + 16 * kq] = 0;
+        d8[col] = 0.0f;
+#pragma unroll
+        for (int sb = 0; sb < 8; ++sb) sums[sb] = 0;
+        return;
+    }
+    const int p = ((const int *) (a.ws + a.ws_list))[row[1] + col];
+    const int t = p / a.n_used, c = p % a.n_used;
+    const uint8_t *blk = a.y + (int64_t) (c % a.nchannels_y) * a.stride_channel_y + (int64_t) t * a.stride_col_y +
+                         (int64_t) s * 292;
+    const uint64_t *qs = (const uint64_t *) (blk + 4);     // q8_K: d (4 B) | qs[256] | bsums[16] int16
+#pragma unroll
+    for (int sb = 0; sb < 8; ++sb)
+#pragma unroll
+        for (int kq = 0; kq < 4; ++kq) frag[sb * 64 + col + 16 * kq] = qs[4 * sb + kq];
+    d8[col] = *(const float *) blk;
+    const int16_t *bs = (const int16_t *) (blk + 260);
+#pragma unroll
+    for (int sb = 0; sb < 8; ++sb) sums[sb] = (int16_t) (bs[2 * sb] + bs[2 * sb + 1]);
+}
+
+// ---------------------------------------------------------------------------
+// 3. grouped GEMM
+// ---------------------------------------------------------------------------
+
+// Issues the DMA of super-block s: MMQ_ROWS weight rows (one 144-byte Q4_K/176-byte
+// Q5_K super-block each, rows row_bytes apart) and nb activation records.
+template <int T>
+__device__ __forceinline__ void mmq_issue(const MmqArgs &a, const uint8_t *wbase, int row0, int s, int blk0, int nb,
+                                          uint8_t *wl, uint8_t *rl) {
+    constexpr int SBB = type_geom(T).block_bytes;           // bytes of one super-block
+    constexpr int CH = SBB / 16;                            // 16-byte chunks per super-block
+    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    const uint32_t row_bytes = (uint32_t) (a.ncols / 256) * SBB;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(wbase, (uint32_t) a.expert_bytes);
+    for (int i = wave; i < CH * MMQ_ROWS / WAVE; i += MMQ_WAVES) {
+        const int q = i * WAVE + lane;                       // chunk q of the tile: row q / CH, part q % CH
+        const uint32_t off = (uint32_t) (row0 + q / CH) * row_bytes + (uint32_t) s * SBB + 16u * (uint32_t) (q % CH);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void_t *) (wl + 1024 * i), 16, off, 0, 0, 0);
+    }
+    const uint8_t *recs = a.ws + a.ws_packed + ((int64_t) s * a.max_blocks + blk0) * MMQ_REC_BYTES;
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(recs, (uint32_t) nb * MMQ_REC_BYTES);
+    const int rounds = (nb * MMQ_REC_BYTES + 1023) / 1024;
+    for (int i = wave; i < rounds; i += MMQ_WAVES)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void_t *) (rl + 1024 * i), 16, 1024u * i + 16u * lane, 0, 0, 0);
+}
+
+__device__ __forceinline__ int mmq_issue_count(int nb, int wave, int ch) {
+    int n = 0;
+    for (int i = wave; i < ch * MMQ_ROWS / WAVE; i += MMQ_WAVES) ++n;
+    for (int i = wave; i < (nb * MMQ_REC_BYTES + 1023) / 1024; i += MMQ_WAVES) ++n;
+    return n;
+}
+
+// d8 * d * isum - d8 * dmin * msum, the q8_K super-block result (products unfused).
+__device__ __forceinline__ float mmq_superblock_value(float d8, float d, float dmin, int isum, int msum) {
+#pragma clang fp contract(off)
+    const float dall = d8 * d, dmn = d8 * dmin;
+    return dall * (float) isum - dmn * (float) msum;
+}
+
+// One super-block of one 16-row weight tile (the wave's rows, lane's row = lane % 16)
+// against nb column blocks: acc[b][i] for pair 4 (lane / 16) + i of block b.
+template <int T>
+__device__ __forceinline__ void mmq_superblock(const uint8_t *wrow, const uint8_t *recs, int nb,
+                                               float (&acc)[MMQ_MAX_BLOCKS][4]) {
+    const int lane = threadIdx.x % WAVE;
+    const int kq = lane / 16;
+    const u32 *w = (const u32 *) wrow;
+    const float d = h2f(w[0]), dmin = h2f(w[0] >> 16);
+    u32 SC0, SC1, M0, M1;
+    kq_scales(w[1], w[2], w[3], SC0, SC1, M0, M1);
+    constexpr bool Q5 = T == T_Q5_K;
+    constexpr int QS = Q5 ? 12 : 4;                         // dword offset of qs[128]
+    long bf[8];                                             // B fragments: 8 weight codes of this row per sub-block
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const u32 q0 = w[QS + 8 * c + 2 * kq], q1 = w[QS + 8 * c + 2 * kq + 1];
+        u32 lo0 = q0 & 0x0F0F0F0Fu, lo1 = q1 & 0x0F0F0F0Fu;
+        u32 hi0 = (q0 >> 4) & 0x0F0F0F0Fu, hi1 = (q1 >> 4) & 0x0F0F0F0Fu;
+        if constexpr (Q5) {                                  // high bit of element l of sub-block g: qh[l] bit g
+            const u32 h0 = w[4 + 2 * kq], h1 = w[4 + 2 * kq + 1];
+            lo0 |= ((h0 >> (2 * c)) & 0x01010101u) << 4;
+            lo1 |= ((h1 >> (2 * c)) & 0x01010101u) << 4;
+            hi0 |= ((h0 >> (2 * c + 1)) & 0x01010101u) << 4;
+            hi1 |= ((h1 >> (2 * c + 1)) & 0x01010101u) << 4;
+        }
+        bf[2 * c] = (long) (((uint64_t) lo1 << 32) | lo0);
+        bf[2 * c + 1] = (long) (((uint64_t) hi1 << 32) | hi0);
+    }
+    int sc[8], mn[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+        sc[g] = (int) byte_of(g < 4 ? SC0 : SC1, g & 3);
+        mn[g] = (int) byte_of(g < 4 ? M0 : M1, g & 3);
+    }
+#pragma unroll
+    for (int b = 0; b < MMQ_MAX_BLOCKS; ++b) {
+        if (b >= nb) break;
+        const uint8_t *rec = recs + b * MMQ_REC_BYTES;
+        const long *af = (const long *) (rec + MMQ_REC_FRAG);
+        int isum[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            const v4i r = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[g * 64 + lane], bf[g], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) isum[i] += __mul24(sc[g], r[i]);
+        }
+        const v4f d8 = *(const v4f *) (rec + MMQ_REC_D8 + 16 * kq);
+        const float d8a[4] = {d8.x, d8.y, d8.z, d8.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int16_t *s16 = (const int16_t *) (rec + MMQ_REC_SUM) + 8 * (4 * kq + i);
+            int msum = 0;
+#pragma unroll
+            for (int g = 0; g < 8; ++g) msum += __mul24(mn[g], (int) s16[g]);
+            acc[b][i] += mmq_superblock_value(d8a[i], d, dmin, isum[i], msum);
+        }
+    }
+}
+
+template <int T, bool GATE>
+__global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const MmqArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr int SBB = type_geom(T).block_bytes;
+    constexpr int CH = SBB / 16;
+    constexpr uint32_t WT = MMQ_ROWS * SBB;                 // weight tile bytes per matrix and super-block
+    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    const int e = blockIdx.y;
+    const int *blk_off = (const int *) (a.ws + a.ws_blk_off);
+    const int blk_first = blk_off[e], nblk = blk_off[e + 1] - blk_first;
+    if (nblk <= 0) return;
+    const int row0 = blockIdx.x * MMQ_ROWS;
+    const int n_sb = a.ncols / 256;
+    const uint8_t *wup = a.w + (int64_t) e * a.expert_bytes;
+    const uint8_t *wgt = GATE ? a.w_gate + (int64_t) e * a.expert_bytes : nullptr;
+    // LDS: two stages of [up tile | gate tile | records]
+    const uint32_t stage = (GATE ? 2u : 1u) * WT + MMQ_MAX_BLOCKS * MMQ_REC_BYTES + 1024u;
+    const int *blk_tab = (const int *) (a.ws + a.ws_blk_tab);
+    const int *list = (const int *) (a.ws + a.ws_list);
+
+    for (int g0 = 0; g0 < nblk; g0 += MMQ_MAX_BLOCKS) {
+        const int nb = min(MMQ_MAX_BLOCKS, nblk - g0);
+        float acc[MMQ_MAX_BLOCKS][4], accg[MMQ_MAX_BLOCKS][4];
+#pragma unroll
+        for (int b = 0; b < MMQ_MAX_BLOCKS; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[b][i] = accg[b][i] = 0.0f;
+        const int per_stage = mmq_issue_count(nb, wave, CH) + (GATE ? mmq_issue_count(0, wave, CH) : 0);
+        auto issue = [&](int s) {
+            uint8_t *st = lds + (uint32_t) (s & 1) * stage;
+            mmq_issue<T>(a, wup, row0, s, blk_first + g0, nb, st, st + (GATE ? 2 : 1) * WT);
+            if (GATE) mmq_issue<T>(a, wgt, row0, s, blk_first + g0, 0, st + WT, nullptr);
+        };
+        issue(0);
+        for (int s = 0; s < n_sb; ++s) {
+            if (s + 1 < n_sb) {
+                issue(s + 1);
+                wait_loads_at_most(per_stage);                // stage s has landed for this wave
+            } else {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+            __syncthreads();                                  // ... and for every wave
+            const uint8_t *st = lds + (uint32_t) (s & 1) * stage;
+            const uint8_t *recs = st + (GATE ? 2 : 1) * WT;
+            const uint32_t roff = (uint32_t) (16 * wave + lane % 16) * SBB;
+            mmq_superblock<T>(st + roff, recs, nb, acc);
+            if (GATE) mmq_superblock<T>(st + WT + roff, recs, nb, accg);
+            __syncthreads();                                  // stage s is free for s + 2
+        }
+        // scatter: pair 4 (lane / 16) + i of each block, weight row lane % 16 of the wave's tile
+        const int row = row0 + 16 * wave + lane % 16;
+        if (row < a.nrows) {
+#pragma unroll
+            for (int b = 0; b < MMQ_MAX_BLOCKS; ++b) {
+                if (b >= nb) break;
+                const int *tab = blk_tab + 4 * (blk_first + g0 + b);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int slot = 4 * (lane / 16) + i;
+                    if (slot >= tab[2]) continue;
+                    const int p = list[tab[1] + slot];
+                    const int t = p / a.n_used, c = p % a.n_used;
+                    const float out = GATE ? glu_apply(a.glu_op, accg[b][i], acc[b][i], a.glu_limit) : acc[b][i];
+                    a.dst[(int64_t) t * a.stride_col_dst + (int64_t) c * a.stride_channel_dst + row] = out;
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// launcher
+// ---------------------------------------------------------------------------
+
+template <int T>
+static hipError_t launch_mmq_t(const MmqArgs &a, hipStream_t s) {
+    constexpr uint32_t WT = MMQ_ROWS * type_geom(T).block_bytes;
+    const bool gate = a.w_gate != nullptr;
+    const uint32_t stage = (gate ? 2u : 1u) * WT + MMQ_MAX_BLOCKS * MMQ_REC_BYTES + 1024u;
+    const dim3 grid((unsigned) ((a.nrows + MMQ_ROWS - 1) / MMQ_ROWS), (unsigned) a.n_experts);
+    // more than the default 64 KiB of dynamic LDS: raise the kernel's limit once
+    static const hipError_t attr_gate = hipFuncSetAttribute((const void *) mc_mmq_gemm_kernel<T, true>,
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int) (2 * (2 * WT + MMQ_MAX_BLOCKS * MMQ_REC_BYTES + 1024u)));
+    static const hipError_t attr_plain = hipFuncSetAttribute((const void *) mc_mmq_gemm_kernel<T, false>,
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int) (2 * (WT + MMQ_MAX_BLOCKS * MMQ_REC_BYTES + 1024u)));
+    if (attr_gate != hipSuccess) return attr_gate;
+    if (attr_plain != hipSuccess) return attr_plain;
+    if (gate) hipLaunchKernelGGL((mc_mmq_gemm_kernel<T, true>), grid, dim3(MMQ_WAVES * WAVE), 2 * stage, s, a);
+    else hipLaunchKernelGGL((mc_mmq_gemm_kernel<T, false>), grid, dim3(MMQ_WAVES * WAVE), 2 * stage, s, a);
+    return hipGetLastError();
+}
+
+// Grouping, activation records and the grouped GEMM; a.ws holds the workspace.
+int launch_mmq(const MmqArgs &a, int type, void *stream) {
+    hipStream_t s = (hipStream_t) stream;
+    if (a.n_tok <= 0 || a.n_used <= 0) return (int) hipSuccess;
+    if (a.n_experts > MMQ_MAX_EXPERTS || a.ncols % 256) return (int) hipErrorInvalidValue;
+    hipLaunchKernelGGL(mc_mmq_group_kernel, dim3(1), dim3(MMQ_GROUP_THREADS), 0, s, a);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return (int) err;
+    const int64_t threads = (int64_t) a.max_blocks * MMQ_COLS * (a.ncols / 256);
+    hipLaunchKernelGGL(mc_mmq_pack_kernel, dim3((unsigned) ((threads + 255) / 256)), dim3(256), 0, s, a);
+    if ((err = hipGetLastError()) != hipSuccess) return (int) err;
+    switch (type) {
+        case T_Q4_K: return (int) launch_mmq_t<T_Q4_K>(a, s);
+        case T_Q5_K: return (int) launch_mmq_t<T_Q5_K>(a, s);
+        default: return (int) hipErrorInvalidValue;
+    }
+}
+
+}  // namespace mc

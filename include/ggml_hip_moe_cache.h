@@ -217,6 +217,33 @@ int ggml_hip_moe_combine_q8_1(const float *o, int64_t o_stride, const float *w, 
 
 
 /* ---------------------------------------------------------------------
+ * Prefill-shaped MUL_MAT_ID (many tokens).  The reference routes only batch-1
+ * decode to its pointer-table GEMV and leaves many-token MUL_MAT_ID to
+ * upstream ggml's MMQ path (results/final.patch:45-48); this is its gfx950
+ * counterpart: the (token, slot) pairs are grouped by expert and multiplied
+ * with int8 MFMA.
+ * --------------------------------------------------------------------- */
+
+/* Bytes of device workspace ggml_hip_moe_mul_mat_q needs for ne00 columns, ne02
+ * experts and n_pairs = tokens * slots (no initialisation required). */
+int64_t ggml_hip_moe_mul_mat_q_workspace_bytes(int64_t ne00, int64_t ne02, int64_t n_pairs);
+
+/* MUL_MAT_ID over device-resident K-quant experts (Q4_K, Q5_K) with q8_K
+ * activations (ggml_hip_quantize_q8_K; the ggml-CPU vec_dot_type of these types):
+ *   dst[t*stride_col_dst + c*stride_channel_dst + r] = W[ids[c + t*ids_stride]][r] . y(t, c)
+ * with y(t, c) the q8_K row (c % nchannels_y)*stride_channel_y + t*stride_col_y (strides in
+ * q8_K blocks of 256 values).  fusion may carry gate (same shape, device) with glu_op/glu_limit:
+ * dst = GLU(gate . y, W . y); other fusion fields are not supported here.  Expert ids outside
+ * [0, ne02) are skipped.  src1 and workspace 256-byte aligned, weights 16-byte aligned. */
+int ggml_hip_moe_mul_mat_q(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_fusion *fusion,
+                           const void *src1_q8_K, const int32_t *ids_d, float *dst_d,
+                           int64_t ne00, int64_t ne01, int64_t ne02,
+                           int64_t ncols_dst, int64_t nchannels_y, int64_t nchannels_dst,
+                           int64_t stride_col_y, int64_t stride_col_dst,
+                           int64_t stride_channel_y, int64_t stride_channel_dst,
+                           int64_t ids_stride, void *workspace, int64_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------
  * Configuration, introspection and teardown (the reference reads env vars
  * once and never frees; kernels/moe-cache.cu:315-363)
  * --------------------------------------------------------------------- */
