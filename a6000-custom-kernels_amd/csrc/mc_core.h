@@ -481,15 +481,21 @@ __device__ __forceinline__ int dma_span(const uint8_t *base, u32 base_bytes, u32
 }
 
 // Waits until at most n of this wave's vector memory loads are outstanding
-// (loads complete in issue order, so every earlier load has landed).
+// (loads complete in issue order, so every earlier load has landed).  vmcnt
+// holds 6 bits: n >= 63 waits for at most 63.
 __device__ __forceinline__ void wait_loads_at_most(int n) {
     switch (n) {
 #define MC_WAITCASE(k) case k: asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); break;
-        MC_WAITCASE(0) MC_WAITCASE(1) MC_WAITCASE(2) MC_WAITCASE(3) MC_WAITCASE(4) MC_WAITCASE(5)
-        MC_WAITCASE(6) MC_WAITCASE(7) MC_WAITCASE(8) MC_WAITCASE(9) MC_WAITCASE(10) MC_WAITCASE(11)
-        MC_WAITCASE(12) MC_WAITCASE(13) MC_WAITCASE(14)
+        MC_WAITCASE(0) MC_WAITCASE(1) MC_WAITCASE(2) MC_WAITCASE(3) MC_WAITCASE(4) MC_WAITCASE(5) MC_WAITCASE(6) MC_WAITCASE(7)
+        MC_WAITCASE(8) MC_WAITCASE(9) MC_WAITCASE(10) MC_WAITCASE(11) MC_WAITCASE(12) MC_WAITCASE(13) MC_WAITCASE(14) MC_WAITCASE(15)
+        MC_WAITCASE(16) MC_WAITCASE(17) MC_WAITCASE(18) MC_WAITCASE(19) MC_WAITCASE(20) MC_WAITCASE(21) MC_WAITCASE(22) MC_WAITCASE(23)
+        MC_WAITCASE(24) MC_WAITCASE(25) MC_WAITCASE(26) MC_WAITCASE(27) MC_WAITCASE(28) MC_WAITCASE(29) MC_WAITCASE(30) MC_WAITCASE(31)
+        MC_WAITCASE(32) MC_WAITCASE(33) MC_WAITCASE(34) MC_WAITCASE(35) MC_WAITCASE(36) MC_WAITCASE(37) MC_WAITCASE(38) MC_WAITCASE(39)
+        MC_WAITCASE(40) MC_WAITCASE(41) MC_WAITCASE(42) MC_WAITCASE(43) MC_WAITCASE(44) MC_WAITCASE(45) MC_WAITCASE(46) MC_WAITCASE(47)
+        MC_WAITCASE(48) MC_WAITCASE(49) MC_WAITCASE(50) MC_WAITCASE(51) MC_WAITCASE(52) MC_WAITCASE(53) MC_WAITCASE(54) MC_WAITCASE(55)
+        MC_WAITCASE(56) MC_WAITCASE(57) MC_WAITCASE(58) MC_WAITCASE(59) MC_WAITCASE(60) MC_WAITCASE(61) MC_WAITCASE(62)
 #undef MC_WAITCASE
-        default: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
+        default: asm volatile("s_waitcnt vmcnt(63)" ::: "memory"); break;
     }
 }
 

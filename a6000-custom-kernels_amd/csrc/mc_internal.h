@@ -178,7 +178,7 @@ constexpr int RMS_CHUNK = 256;
 constexpr int MMQ_COLS = 16;              // (token, slot) pairs per column block: the MFMA M dimension
 constexpr int MMQ_WAVES = 4;              // waves per GEMM workgroup, 16 weight rows each
 constexpr int MMQ_ROWS = 16 * MMQ_WAVES;  // weight rows per GEMM workgroup
-constexpr int MMQ_MAX_BLOCKS = 4;         // column blocks multiplied per pass over an expert's weights
+constexpr int MMQ_MAX_BLOCKS = 2;         // column blocks multiplied per pass over an expert's weights
 constexpr int MMQ_MAX_EXPERTS = 4096;
 constexpr int MMQ_REC_BYTES = 4416;       // activation record of one (super-block, column block)
 

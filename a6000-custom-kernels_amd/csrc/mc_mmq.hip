@@ -219,62 +219,103 @@ __device__ __forceinline__ float mmq_superblock_value(float d8, float d, float d
     return dall * (float) isum - dmn * (float) msum;
 }
 
-// One super-block of one 16-row weight tile (the wave's rows, lane's row = lane % 16)
-// against nb column blocks: acc[b][i] for pair 4 (lane / 16) + i of block b.
-template <int T>
-__device__ __forceinline__ void mmq_superblock(const uint8_t *wrow, const uint8_t *recs, int nb,
-                                               float (&acc)[MMQ_MAX_BLOCKS][4]) {
-    const int lane = threadIdx.x % WAVE;
-    const int kq = lane / 16;
-    const u32 *w = (const u32 *) wrow;
-    const float d = h2f(w[0]), dmin = h2f(w[0] >> 16);
+// Decoded scale words of one K-quant row super-block (Q4_K/Q5_K): d, dmin and the
+// packed 6-bit sub-block scales and mins (kq_scales).
+struct RowScales {
+    float d, dmin;
     u32 SC0, SC1, M0, M1;
-    kq_scales(w[1], w[2], w[3], SC0, SC1, M0, M1);
+};
+
+__device__ __forceinline__ RowScales row_scales(const u32 *w) {
+    RowScales r;
+    r.d = h2f(w[0]);
+    r.dmin = h2f(w[0] >> 16);
+    kq_scales(w[1], w[2], w[3], r.SC0, r.SC1, r.M0, r.M1);
+    return r;
+}
+
+// B fragments of sub-blocks 2c and 2c+1 for this lane (weight row lane % 16, values
+// 8 (lane / 16) .. +7 of each sub-block) from the row's super-block at w.
+template <int T>
+__device__ __forceinline__ void row_frags(const u32 *w, int c, int kq, long &lo, long &hi) {
     constexpr bool Q5 = T == T_Q5_K;
     constexpr int QS = Q5 ? 12 : 4;                         // dword offset of qs[128]
-    long bf[8];                                             // B fragments: 8 weight codes of this row per sub-block
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const u32 q0 = w[QS + 8 * c + 2 * kq], q1 = w[QS + 8 * c + 2 * kq + 1];
-        u32 lo0 = q0 & 0x0F0F0F0Fu, lo1 = q1 & 0x0F0F0F0Fu;
-        u32 hi0 = (q0 >> 4) & 0x0F0F0F0Fu, hi1 = (q1 >> 4) & 0x0F0F0F0Fu;
-        if constexpr (Q5) {                                  // high bit of element l of sub-block g: qh[l] bit g
-            const u32 h0 = w[4 + 2 * kq], h1 = w[4 + 2 * kq + 1];
-            lo0 |= ((h0 >> (2 * c)) & 0x01010101u) << 4;
-            lo1 |= ((h1 >> (2 * c)) & 0x01010101u) << 4;
-            hi0 |= ((h0 >> (2 * c + 1)) & 0x01010101u) << 4;
-            hi1 |= ((h1 >> (2 * c + 1)) & 0x01010101u) << 4;
-        }
-        bf[2 * c] = (long) (((uint64_t) lo1 << 32) | lo0);
-        bf[2 * c + 1] = (long) (((uint64_t) hi1 << 32) | hi0);
+    const u32 q0 = w[QS + 8 * c + 2 * kq], q1 = w[QS + 8 * c + 2 * kq + 1];
+    u32 lo0 = q0 & 0x0F0F0F0Fu, lo1 = q1 & 0x0F0F0F0Fu;
+    u32 hi0 = (q0 >> 4) & 0x0F0F0F0Fu, hi1 = (q1 >> 4) & 0x0F0F0F0Fu;
+    if constexpr (Q5) {                                      // high bit of element l of sub-block g: qh[l] bit g
+        const u32 h0 = w[4 + 2 * kq], h1 = w[4 + 2 * kq + 1];
+        lo0 |= ((h0 >> (2 * c)) & 0x01010101u) << 4;
+        lo1 |= ((h1 >> (2 * c)) & 0x01010101u) << 4;
+        hi0 |= ((h0 >> (2 * c + 1)) & 0x01010101u) << 4;
+        hi1 |= ((h1 >> (2 * c + 1)) & 0x01010101u) << 4;
     }
-    int sc[8], mn[8];
+    lo = (long) (((uint64_t) lo1 << 32) | lo0);
+    hi = (long) (((uint64_t) hi1 << 32) | hi0);
+}
+
+// Sub-block products of one matrix against one column block, accumulated into isum.
+__device__ __forceinline__ void mmq_mfma_pair(long a_lo, long a_hi, long b_lo, long b_hi, u32 SC, int c,
+                                              int (&isum)[4]) {
+    const v4i rl = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, b_lo, v4i{0, 0, 0, 0}, 0, 0, 0);
+    const v4i rh = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, b_hi, v4i{0, 0, 0, 0}, 0, 0, 0);
+    const int sl = (int) byte_of(SC, (2 * c) & 3), sh = (int) byte_of(SC, (2 * c + 1) & 3);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) isum[i] += __mul24(sl, rl[i]) + __mul24(sh, rh[i]);
+}
+
+// Sum of the eight sub-block mins (bytes of M0, M1) times a pair's 32-value code
+// sums (eight int16 in s4).
+__device__ __forceinline__ int mins_dot(u32 M0, u32 M1, const v4u s4) {
+    const u32 sw[4] = {s4.x, s4.y, s4.z, s4.w};
+    int r = 0;
 #pragma unroll
     for (int g = 0; g < 8; ++g) {
-        sc[g] = (int) byte_of(g < 4 ? SC0 : SC1, g & 3);
-        mn[g] = (int) byte_of(g < 4 ? M0 : M1, g & 3);
+        const int sv = (int) (int16_t) (sw[g >> 1] >> (16 * (g & 1)));
+        r += __mul24((int) byte_of(g < 4 ? M0 : M1, g & 3), sv);
     }
+    return r;
+}
+
+// One super-block of one 16-row weight tile (the wave's rows, the lane's row =
+// lane % 16) of the up matrix (and the gate) against nb column blocks: acc[b][i]
+// for pair 4 (lane / 16) + i of block b.
+template <int T, bool GATE>
+__device__ __forceinline__ void mmq_superblock(const uint8_t *wrow_up, const uint8_t *wrow_gate, const uint8_t *recs,
+                                               int nb, float (&acc)[MMQ_MAX_BLOCKS][4],
+                                               float (&accg)[MMQ_MAX_BLOCKS][4]) {
+    const int lane = threadIdx.x % WAVE;
+    const int kq = lane / 16;
+    const u32 *wu = (const u32 *) wrow_up;
+    const u32 *wg = (const u32 *) wrow_gate;
+    const RowScales su = row_scales(wu);
+    RowScales sg{};
+    if constexpr (GATE) sg = row_scales(wg);
 #pragma unroll
     for (int b = 0; b < MMQ_MAX_BLOCKS; ++b) {
         if (b >= nb) break;
         const uint8_t *rec = recs + b * MMQ_REC_BYTES;
         const long *af = (const long *) (rec + MMQ_REC_FRAG);
-        int isum[4] = {0, 0, 0, 0};
+        int iu[4] = {0, 0, 0, 0}, ig[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            const v4i r = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[g * 64 + lane], bf[g], v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) isum[i] += __mul24(sc[g], r[i]);
+        for (int c = 0; c < 4; ++c) {
+            const long a_lo = af[(2 * c) * 64 + lane], a_hi = af[(2 * c + 1) * 64 + lane];
+            long b_lo, b_hi;
+            row_frags<T>(wu, c, kq, b_lo, b_hi);
+            mmq_mfma_pair(a_lo, a_hi, b_lo, b_hi, c < 2 ? su.SC0 : su.SC1, c, iu);
+            if constexpr (GATE) {
+                row_frags<T>(wg, c, kq, b_lo, b_hi);
+                mmq_mfma_pair(a_lo, a_hi, b_lo, b_hi, c < 2 ? sg.SC0 : sg.SC1, c, ig);
+            }
         }
         const v4f d8 = *(const v4f *) (rec + MMQ_REC_D8 + 16 * kq);
         const float d8a[4] = {d8.x, d8.y, d8.z, d8.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int16_t *s16 = (const int16_t *) (rec + MMQ_REC_SUM) + 8 * (4 * kq + i);
-            int msum = 0;
-#pragma unroll
-            for (int g = 0; g < 8; ++g) msum += __mul24(mn[g], (int) s16[g]);
-            acc[b][i] += mmq_superblock_value(d8a[i], d, dmin, isum[i], msum);
+            const v4u s4 = *(const v4u *) (rec + MMQ_REC_SUM + 16 * (4 * kq + i));
+            acc[b][i] += mmq_superblock_value(d8a[i], su.d, su.dmin, iu[i], mins_dot(su.M0, su.M1, s4));
+            if constexpr (GATE)
+                accg[b][i] += mmq_superblock_value(d8a[i], sg.d, sg.dmin, ig[i], mins_dot(sg.M0, sg.M1, s4));
         }
     }
 }
@@ -324,8 +365,7 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
             const uint8_t *st = lds + (uint32_t) (s & 1) * stage;
             const uint8_t *recs = st + (GATE ? 2 : 1) * WT;
             const uint32_t roff = (uint32_t) (16 * wave + lane % 16) * SBB;
-            mmq_superblock<T>(st + roff, recs, nb, acc);
-            if (GATE) mmq_superblock<T>(st + WT + roff, recs, nb, accg);
+            mmq_superblock<T, GATE>(st + roff, st + WT + roff, recs, nb, acc, accg);
             __syncthreads();                                  // stage s is free for s + 2
         }
         // scatter: pair 4 (lane / 16) + i of each block, weight row lane % 16 of the wave's tile
