@@ -10,14 +10,18 @@
          seeded routings per point;
   cfg5a  the prefill-shaped FFN: 512 tokens x top-8 over 512 Q4_K experts through
          the expert-grouped int8-MFMA path (q8_K of x, gate/up + SwiGLU, q8_K of
-         the GLU rows, down).
+         the GLU rows, down);
+  cfg3   the pointer-table cache under mixed residency: 40 layers of Q2_K experts
+         (63 GB) in pinned host memory, an HBM pool holding 435 of 512 experts per
+         tensor, Zipf(1.1) routing, 256 decode tokens with the miss log and LRU
+         step between tokens, calibrated by all-hit and all-miss runs.
 
 Kernel times come from graph replays timed with HIP events on the replay
 stream, so host launch cost is excluded.  Bytes are algorithmic: the unique
 expert matrices a launch touches plus activations and outputs.  cpu_baseline
 (cfg1) is the CPU oracle's ggml-CPU MUL_MAT_ID restatement on this host.
 
-Usage: python bench_configs.py [--configs cfg1,cfg4,cfg5a] [--rounds N]
+Usage: python bench_configs.py [--configs cfg1,cfg3,cfg4,cfg5a] [--rounds N]
 """
 from __future__ import annotations
 
@@ -196,6 +200,150 @@ def cfg5a(torch, mc, md, rounds):
           "tok_per_s": round(T / (ms_all * 1e-3), 1)})
 
 
+def _hip_runtime(torch):
+    """The HIP runtime torch loaded (pinned allocations of exact size, raw copies)."""
+    lib = C.CDLL(os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so"))
+    lib.hipHostMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t, C.c_uint]
+    lib.hipHostMalloc.restype = C.c_int
+    lib.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    lib.hipMemcpy.restype = C.c_int
+    return lib
+
+
+def cfg3(torch, mc, md, rounds, tokens=256, calib_tokens=32, layers=40):
+    """Pointer-table cache under mixed residency: 40 layers (the GPU-mappable pinned host memory
+    of the measurement box ends near 70 GB; 48 layers need 76 GB) of Q2_K gate/up/down experts in
+    pinned host memory, an HBM pool of 435 of each tensor's 512 experts seeded from the head of
+    a seeded per-layer permutation, Zipf(1.1) routing over that permutation, the cache step
+    (miss log, LRU promotion) between tokens.  Calibrated by an all-hit and an all-miss run."""
+    import numpy as np
+    E, H, F, U, POOL = 512, 4096, 768, 8, 435
+    t = mc.Q2_K
+    eb = mc.row_bytes(t, H) * F
+    assert eb == mc.row_bytes(t, F) * H
+    torch.cuda.init()
+    torch.cuda.synchronize()
+    hip = _hip_runtime(torch)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(41)
+    keep, tens = [], {}
+    t0 = time.perf_counter()
+    for l in range(layers):
+        for role, rows, k in (("gate", F, H), ("up", F, H), ("down", H, F)):
+            p = C.c_void_p()
+            rc = hip.hipHostMalloc(C.byref(p), E * eb, 0)
+            assert rc == 0, f"hipHostMalloc of {E * eb} bytes returned {rc} after {len(tens)} tensors"
+            dev = md.random_expert_tensor(torch, t, E, rows, k, gen)
+            torch.cuda.synchronize()
+            assert hip.hipMemcpy(p, C.c_void_p(dev.data_ptr()), E * eb, 2) == 0, "hipMemcpy D2H"
+            del dev
+            tens[(l, role)] = mc.make_tensor(t, k, rows, E, p.value, name=f"blk.{l}.ffn_{role}_exps.weight", keep=keep)
+    log(f"cfg3: {3 * layers} expert tensors ({3 * layers * E * eb / 2**30:.1f} GiB) in pinned host memory, "
+        f"{time.perf_counter() - t0:.1f}s")
+    rng = np.random.default_rng(42)
+    perms = [rng.permutation(E) for _ in range(layers)]
+    logp = -1.1 * np.log(np.arange(1, E + 1))
+
+    def route(n):                                    # Gumbel-top-8 over log p_k: Zipf(1.1) without replacement
+        ids = np.empty((n, layers, U), np.int32)
+        for i in range(n):
+            for l in range(layers):
+                ranks = np.argpartition(-(logp + rng.gumbel(size=E)), U)[:U]
+                ids[i, l] = perms[l][ranks]
+        return ids
+
+    def seed_file(path, n_top):
+        with open(path, "w") as f:
+            for l in range(layers):
+                head = ",".join(str(int(e)) for e in perms[l][:n_top])
+                for role in ("gate", "up", "down"):
+                    f.write(f"blk.{l}.ffn_{role}_exps.weight {head}\n")
+        return path
+
+    lib = mc.lib()
+    s = torch.cuda.Stream()
+    x = torch.randn((1, H), generator=gen, device="cuda")
+    y = mc.quantize_q8_1(x)
+    h = torch.zeros((U, F), dtype=torch.float32, device="cuda")
+    o = torch.zeros((U, H), dtype=torch.float32, device="cuda")
+    ids_dev = torch.zeros((layers, U), dtype=torch.int32, device="cuda")
+    ar = H // 32
+
+    def token(stream):
+        sp = C.c_void_p(stream.cuda_stream)
+        for l in range(layers):
+            mc.check(lib.ggml_hip_moe_cache_mul_mat_vec_q(
+                C.byref(tens[(l, "up")]), C.byref(tens[(l, "gate")]), None, y.data_ptr(), ids_dev[l].data_ptr(),
+                h.data_ptr(), H, F, E, 1, 1, H // 256, eb, eb * E, 1, U, ar, U * F, ar, F, U, sp), "gate/up")
+            mc.check(lib.ggml_hip_moe_mul_mat_vec_ex(
+                1, mc.ACT_F32, C.byref(tens[(l, "down")]), None, None, h.data_ptr(), ids_dev[l].data_ptr(),
+                o.data_ptr(), F, H, E, 1, U, U, U * F, U * H, F, H, U, sp), "down")
+
+    def run(tag, slots, n_top, n_tok, max_promotions):
+        mc.reset()
+        path = seed_file(f"/tmp/moe_seed_{tag}.txt", n_top) if n_top else None
+        mc.configure(enabled=True, slots=slots, budget_gb=0.0, margin_gb=2.0, seed_path=path,
+                     max_promotions=max_promotions)
+        ids = route(n_tok + 1)
+        ids_t = torch.from_numpy(ids).cuda()
+        with torch.cuda.stream(s):
+            ids_dev.copy_(ids_t[0])
+            t_reg = time.perf_counter()
+            token(s)                                 # registration, pool allocation and seeding
+            s.synchronize()
+            t_reg = time.perf_counter() - t_reg
+            mc.check(lib.ggml_hip_moe_cache_step(C.c_void_p(s.cuda_stream)), "step")
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                token(s)
+            s.synchronize()
+            base = mc.totals()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            gpu_ms, step_s = 0.0, 0.0
+            t_all = time.perf_counter()
+            for i in range(1, n_tok + 1):
+                ids_dev.copy_(ids_t[i])
+                e0.record(s)
+                g.replay()
+                e1.record(s)
+                s.synchronize()
+                gpu_ms += e0.elapsed_time(e1)
+                ts = time.perf_counter()
+                mc.check(lib.ggml_hip_moe_cache_step(C.c_void_p(s.cuda_stream)), "step")
+                step_s += time.perf_counter() - ts
+            t_all = time.perf_counter() - t_all
+        tot = mc.totals()
+        hits, misses = tot.hits - base.hits, tot.misses - base.misses
+        picks = hits + misses
+        return {"tokens": n_tok, "slots": slots, "hits": int(hits), "misses": int(misses),
+                "hit_rate": round(hits / max(picks, 1), 4), "promotions": int(tot.promotions - base.promotions),
+                "evictions": int(tot.evictions - base.evictions), "us_per_token_gpu": round(gpu_ms * 1000 / n_tok, 1),
+                "us_per_token_step": round(step_s * 1e6 / n_tok, 1), "us_per_token_wall": round(t_all * 1e6 / n_tok, 1),
+                "registration_s": round(t_reg, 2), "bytes_per_token": int(picks / n_tok * eb)}
+
+    hit = run("allhit", E, E, calib_tokens, 0)
+    hit_gbs = hit["bytes_per_token"] / (hit["us_per_token_gpu"] * 1e-6) / 1e9
+    emit({"config": "cfg3", "run": "calibration, every expert in the HBM pool", **hit, "HBM_GB/s": round(hit_gbs, 1)})
+    miss = run("allmiss", 1, 0, calib_tokens, 0)
+    miss_gbs = miss["bytes_per_token"] / (miss["us_per_token_gpu"] * 1e-6) / 1e9
+    emit({"config": "cfg3", "run": "calibration, every expert read zero-copy from pinned host memory", **miss,
+          "PCIe_GB/s": round(miss_gbs, 2)})
+    mix = run("mixed", POOL, POOL, tokens, 48)
+    # time split: hit bytes at the all-hit rate, the rest of the GPU time is spent on misses
+    hit_bytes = mix["hits"] / mix["tokens"] * eb
+    miss_bytes = mix["misses"] / mix["tokens"] * eb
+    t_hit = hit_bytes / (hit_gbs * 1e9)
+    t_miss = max(mix["us_per_token_gpu"] * 1e-6 - t_hit, 1e-9)
+    emit({"config": "cfg3", "run": f"{layers} layers, pool 435/512 per tensor seeded from the permutation head, "
+                                   "Zipf(1.1) routing, miss log + LRU step between tokens", **mix,
+          "layers": layers, "us_per_layer_gpu": round(mix["us_per_token_gpu"] / layers, 2),
+          "HBM_GB/s_hits": round(hit_gbs, 1),
+          "PCIe_GB/s_misses": round(miss_bytes / t_miss / 1e9, 2) if miss_bytes else None,
+          "tok_per_s_gpu": round(1e6 / mix["us_per_token_gpu"], 1),
+          "tok_per_s_with_step": round(1e6 / mix["us_per_token_wall"], 1)})
+    mc.reset()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--configs", default="cfg1,cfg4,cfg5a")
@@ -207,7 +355,7 @@ def main():
     assert torch.cuda.is_available(), "bench_configs.py needs a HIP device"
     for name in args.configs.split(","):
         log(f"running {name}")
-        {"cfg1": cfg1, "cfg4": cfg4, "cfg5a": cfg5a}[name](torch, mc, md, args.rounds)
+        {"cfg1": cfg1, "cfg3": cfg3, "cfg4": cfg4, "cfg5a": cfg5a}[name](torch, mc, md, args.rounds)
 
 
 if __name__ == "__main__":
