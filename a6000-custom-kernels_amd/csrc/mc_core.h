@@ -465,7 +465,10 @@ template <int T>
 __device__ __forceinline__ int dma_span(const uint8_t *base, u32 base_bytes, u32 start, u32 nbytes, uint8_t *lds) {
     const uintptr_t abase = (uintptr_t) base & ~(uintptr_t) 15;
     const u32 skew = (u32) ((uintptr_t) base - abase);
-    const __amdgpu_buffer_rsrc_t r = make_rsrc((const void *) abase, base_bytes + skew);
+    // the descriptor ends with the span (rounded up to its 16-byte chunk): the lanes of the
+    // last round that lie past it read zeros instead of fetching the next step's rows
+    const u32 end = min(base_bytes + skew, (start + skew + nbytes + 15u) & ~15u);
+    const __amdgpu_buffer_rsrc_t r = make_rsrc((const void *) abase, end);
     const u32 a0 = (start + skew) & ~15u;
     const u32 lead = (start + skew) - a0;
     const int rounds = (int) ((lead + nbytes + 1023u) >> 10);
@@ -526,7 +529,8 @@ __device__ __forceinline__ float row_group_sum(float v, int nu) {
 __device__ __forceinline__ u32 dma_bytes(const uint8_t *base, u32 base_bytes, u32 off, u32 nbytes, uint8_t *lds) {
     const uintptr_t abase = (uintptr_t) base & ~(uintptr_t) 15;
     const u32 skew = (u32) ((uintptr_t) base - abase);
-    const __amdgpu_buffer_rsrc_t r = make_rsrc((const void *) abase, base_bytes + skew);
+    const u32 end = min(base_bytes + skew, (off + skew + nbytes + 15u) & ~15u);   // no fetch past the range
+    const __amdgpu_buffer_rsrc_t r = make_rsrc((const void *) abase, end);
     const u32 a0 = (off + skew) & ~15u;
     const u32 lead = (off + skew) - a0;
     const int rounds = (int) ((lead + nbytes + 1023u) >> 10);

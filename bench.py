@@ -72,6 +72,38 @@ def time_kernel(torch, model, launch, n_rounds):
     return e0.elapsed_time(e1) / n, n
 
 
+def traffic_probe(torch, model, md):
+    """Kernels whose per-dispatch FETCH_SIZE / WRITE_SIZE a counter run reads: three copies of
+    1 GiB (known traffic: 1 GiB read, 1 GiB written) and two gate/up GEMV launches per layer."""
+    n = 1 << 28
+    a, b = torch.empty(n, dtype=torch.float32, device="cuda"), torch.empty(n, dtype=torch.float32, device="cuda")
+    a.fill_(1.0)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        b.copy_(a)
+    ids_np, w_np = md.make_routing(1, model.L, model.E, model.U, seed=7)
+    model.set_routing(torch.from_numpy(ids_np[0]).cuda(), torch.from_numpy(w_np[0]).cuda())
+    model.launch_token()                     # builds every device table
+    torch.cuda.synchronize()
+    for _ in range(2):
+        for l in range(model.L):
+            model.launch_gate_up(l)
+    torch.cuda.synchronize()
+    log(f"traffic probe done: copy {4 * n} bytes x3, gate/up GEMV x{2 * model.L}")
+
+
+def load_traffic():
+    """Per-launch HBM traffic of the gate/up GEMV from the committed counter summary, or None."""
+    p = ROOT / "profiles" / "gemv_gate_up_q2K_traffic.json"
+    if not p.exists():
+        return None
+    try:
+        d = json.loads(p.read_text())
+        return int(d["hbm_bytes_per_launch"])
+    except (ValueError, KeyError):
+        return None
+
+
 def cpu_baseline(torch, model, ids, w, budget_s=12.0):
     """ggml-CPU MUL_MAT_ID restatement (oracle) over layer 0's weights, on this host's cores."""
     import numpy as np
@@ -118,6 +150,9 @@ def main():
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-rounds", type=int, default=10)
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="for rocprofv3 --pmc runs: a 1 GiB copy (the counter calibration) and the gate/up "
+                         "GEMV of every layer, then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not run "
@@ -136,6 +171,9 @@ def main():
     torch.cuda.synchronize()
     log(f"weights ready: {args.layers} layers in {time.perf_counter() - t0:.1f}s, "
         f"{torch.cuda.memory_allocated() / 2**30:.1f} GiB allocated")
+    if args.traffic_probe:
+        traffic_probe(torch, model, md)
+        return
     n_tok_routes = max(64, args.warmup + args.steps)
     ids_np, w_np = md.make_routing(n_tok_routes, model.L, model.E, model.U, seed=7)
     ids_dev = torch.from_numpy(ids_np).cuda()
@@ -206,7 +244,7 @@ def main():
         "tok_per_s": round(tok_s, 2),
         "bytes_per_step": bpt,
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": load_traffic(),
                      "kernel": "mc_gemv_kernel<q2_K, q4_K shared, q8_1> (fused gate/up + SwiGLU)",
                      "bytes_per_launch": gu_bytes, "us_per_launch": round(gu_ms * 1000, 3)},
         "kernels": {"down_gemv": {"bytes_per_launch": dn_bytes, "us_per_launch": round(dn_ms * 1000, 3),
