@@ -91,6 +91,12 @@ SIGNATURES = [
     ("ggml_hip_quantize_q8_0_as_q8_1", C.c_int, [_VP, _VP, _I64, _I64, _I64, _I64, _VP]),
     ("ggml_hip_moe_combine_q8_1", C.c_int,
      [_VP, _I64, _VP, _I32, _VP, _I64, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP, C.c_float, _VP]),
+    ("ggml_hip_moe_ffn_gate_up_norm", C.c_int,
+     [C.c_int, C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Fusion), _VP, _VP, C.c_float, _VP, _VP]
+     + [_I64] * 3 + [_I64] * 2 + [_I64] * 4 + [_VP, _I64, _VP]),
+    ("ggml_hip_moe_ffn_down_combine", C.c_int,
+     [C.c_int, C.c_int, C.POINTER(Tensor), C.POINTER(Fusion), _VP, _VP, _VP, _VP, _VP]
+     + [_I64] * 3 + [_I64] * 2 + [_I64] * 4 + [_VP]),
     ("ggml_hip_moe_mul_mat_q_workspace_bytes", C.c_int64, [_I64, _I64, _I64]),
     ("ggml_hip_moe_mul_mat_q", C.c_int,
      [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _I64, _VP]),
@@ -254,6 +260,47 @@ def mul_mat_vec(*, wtype, weights, ids, y, dst, K, R, n_experts, use_cache=False
         nchannels_y * act_row, n_used * R, act_row, R, ids.stride(0), _stream(stream))
     check(rc, "mul_mat_vec")
     return dst
+
+
+def ffn_gate_up_norm(*, wtype, weights, ids, x, dst, K, R, n_experts, norm_weight=None, eps=1e-6,
+                     fusion: Fusion | None = None, y_out=None, use_cache=False, gate_host=None, name="", stream=None,
+                     weights_ptr=None, gate_ptr=None):
+    """Gate/up GEMV whose q8_1 activation is RMSNorm(x) * norm_weight, computed in the same launch
+    (ggml_hip_moe_ffn_gate_up_norm).  x: fp32 [n_tok, K] (device, 16-byte aligned rows);
+    ids: int32 [n_tok, n_used]; dst: float32 [n_tok, n_used, R]; y_out: optional uint8 [n_tok, K/32*36]."""
+    n_tok, n_used = ids.shape
+    _require_gpu(ids, x, dst, norm_weight, y_out)
+    keep = []
+    ptr = weights_ptr if weights_ptr is not None else weights.data_ptr()
+    src0 = make_tensor(wtype, K, R, n_experts, ptr, name=name, keep=keep)
+    g = make_tensor(wtype, K, R, n_experts, gate_ptr, name=name.replace("up", "gate"), keep=keep) if gate_ptr else None
+    rc = lib().ggml_hip_moe_ffn_gate_up_norm(
+        1 if use_cache else 0, C.byref(src0), C.byref(g) if g is not None else None,
+        C.byref(fusion) if fusion is not None else None, x.data_ptr(), _ptr(norm_weight), eps, ids.data_ptr(),
+        dst.data_ptr(), K, R, n_experts, n_tok, n_used, x.stride(0), n_used * R, R, ids.stride(0),
+        _ptr(y_out), y_out.stride(0) // 36 if y_out is not None else 0, _stream(stream))
+    check(rc, "ffn_gate_up_norm")
+    return dst
+
+
+def ffn_down_combine(*, wtype, weights, ids, h, router_w, x_out, K, R, n_experts, residual=None, act=ACT_F32,
+                     fusion: Fusion | None = None, use_cache=False, name="", stream=None, weights_ptr=None):
+    """Down GEMV over every pick plus the shared expert, combined into x_out = residual + shared +
+    sum_c router_w[c] * o_c in the same launch (ggml_hip_moe_ffn_down_combine).
+    h: pick rows [n_tok, n_used, K] fp32 (act=ACT_F32) or q8_1 blocks [n_tok, n_used, K/32*36];
+    router_w: fp32 [n_tok, n_used]; x_out / residual: fp32 [n_tok, R]."""
+    n_tok, n_used = ids.shape
+    _require_gpu(ids, h, router_w, x_out, residual)
+    keep = []
+    ptr = weights_ptr if weights_ptr is not None else weights.data_ptr()
+    src0 = make_tensor(wtype, K, R, n_experts, ptr, name=name, keep=keep)
+    unit = 1 if act == ACT_F32 else 36          # h strides in floats or in q8_1 blocks
+    rc = lib().ggml_hip_moe_ffn_down_combine(
+        1 if use_cache else 0, act, C.byref(src0), C.byref(fusion) if fusion is not None else None, h.data_ptr(),
+        ids.data_ptr(), router_w.data_ptr(), _ptr(residual), x_out.data_ptr(), K, R, n_experts, n_tok, n_used,
+        h.stride(0) // unit, h.stride(1) // unit, x_out.stride(0), ids.stride(0), _stream(stream))
+    check(rc, "ffn_down_combine")
+    return x_out
 
 
 def mul_mat_q(*, wtype, weights, ids, y, dst, K, R, n_experts, gate=None, glu_op=GLU_SWIGLU, glu_limit=0.0,

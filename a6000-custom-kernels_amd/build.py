@@ -37,6 +37,7 @@ HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function"]
 SOURCES = [
     ("mc_kernels.hip", "hip"),
     ("mc_mmq.hip", "hip"),
+    ("mc_ffn.hip", "hip"),
     ("mc_device_hip.cpp", "hiphost"),
     ("mc_host.cpp", "cxx"),
 ]

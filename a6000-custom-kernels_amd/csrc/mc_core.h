@@ -651,6 +651,21 @@ __device__ __forceinline__ void quantize_row_lds(const float *x, uint8_t *q, int
     wave_lds_sync();
 }
 
+// Sum of squares of one 256-value chunk in the canonical RMS order (mc_internal.h):
+// lane l holds values 4l .. 4l+3 of the chunk in xv; returned in every lane.
+__device__ __forceinline__ float rms_chunk_sum(const float xv[4]) {
+    const int lane = threadIdx.x % WAVE;
+    float a = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a = fmaf(xv[k], xv[k], a);
+#pragma unroll
+    for (int off = WAVE / 2; off > 0; off >>= 1) {
+        const float other = __shfl_down(a, off, WAVE);
+        if (lane < off) a += other;
+    }
+    return __shfl(a, 0, WAVE);
+}
+
 constexpr int COMBINE_MAX_USED = 16;
 
 // One 64-lane wave: the 256 combined values of chunk j of a row, lane l holding
@@ -692,15 +707,17 @@ __device__ __forceinline__ float combine_chunk(const float *o, int64_t o_stride,
     xv[1] = x.y;
     xv[2] = x.z;
     xv[3] = x.w;
-    float a = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) a = fmaf(xv[k], xv[k], a);
-#pragma unroll
-    for (int off = WAVE / 2; off > 0; off >>= 1) {
-        const float other = __shfl_down(a, off, WAVE);
-        if (lane < off) a += other;
-    }
-    return __shfl(a, 0, WAVE);
+    return rms_chunk_sum(xv);
+}
+
+// Maximum over the 8-lane group of each lane (lanes 8g .. 8g+7): quad exchanges by DPP,
+// the exchange between the two quads of the group by ds_swizzle (xor 4).  fmaxf is exact,
+// so the result equals any other reduction order.
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x101F)));
+    return v;
 }
 
 // One 64-lane wave: q8_1 of the 256 values v of chunk j into y (row base), lane l
@@ -709,6 +726,8 @@ __device__ __forceinline__ float combine_chunk(const float *o, int64_t o_stride,
 // arithmetic is the q8_1 quantizer's (q8_1_lane): amax, d = amax / 127,
 // code = amax == 0 ? 0 : roundf(v / d), and the block sum in the quantizer's
 // xor-butterfly order (offsets 16, 8, 4 across lanes, then 2, 1 inside the lane).
+// WITH_SUM = false leaves the sum field 0: the K-quant dots read only d and the codes.
+template <bool WITH_SUM = true>
 __device__ __forceinline__ void quantize_chunk(const float xv[4], bool norm, float s, const v4f nwv, uint8_t *y,
                                                int j) {
     const int lane = threadIdx.x % WAVE;
@@ -718,17 +737,18 @@ __device__ __forceinline__ void quantize_chunk(const float xv[4], bool norm, flo
 #pragma unroll
         for (int k = 0; k < 4; ++k) v[k] = (v[k] * s) * nw[k];
     }
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    const float amax = max8(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+    float sum = 0.0f;
+    if constexpr (WITH_SUM) {
+        float t[4] = {v[0], v[1], v[2], v[3]};
 #pragma unroll
-    for (int off = 4; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, WAVE));
-    float t[4] = {v[0], v[1], v[2], v[3]};
+        for (int off = 4; off > 0; off >>= 1) {
 #pragma unroll
-    for (int off = 4; off > 0; off >>= 1) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) t[k] += __shfl_xor(t[k], off, WAVE);
+            for (int k = 0; k < 4; ++k) t[k] += __shfl_xor(t[k], off, WAVE);
+        }
+        const float t2[4] = {t[0] + t[2], t[1] + t[3], t[2] + t[0], t[3] + t[1]};
+        sum = t2[0] + t2[1];
     }
-    const float t2[4] = {t[0] + t[2], t[1] + t[3], t[2] + t[0], t[3] + t[1]};
-    const float sum = t2[0] + t2[1];
     const float d = amax / 127.0f;
     u32 packed = 0;
 #pragma unroll
@@ -739,7 +759,7 @@ __device__ __forceinline__ void quantize_chunk(const float xv[4], bool norm, flo
     const int i = j * RMS_CHUNK + 4 * lane;               // first value of this lane in the row
     uint8_t *yb = y + (i / 32) * 36;
     *(u32 *) (yb + 4 + (i % 32)) = packed;
-    if ((lane & 7) == 0) *(u32 *) yb = (u32) f2h_bits(d) | ((u32) f2h_bits(sum) << 16);
+    if ((lane & 7) == 0) *(u32 *) yb = (u32) f2h_bits(d) | (WITH_SUM ? ((u32) f2h_bits(sum) << 16) : 0u);
 }
 
 }  // namespace mc

@@ -1,0 +1,399 @@
+// mc_ffn.hip -- fused decode kernels for one MoE FFN block (a few tokens).
+//
+// ggml evaluates a MoE block as RMS_NORM -> MUL(norm weight) -> quantize_q8_1 ->
+// MUL_MAT_ID(gate, up) + GLU -> quantize -> MUL_MAT_ID(down) -> MUL(router
+// weights) -> sum over slots -> ADD(shared expert) -> ADD(residual).  The
+// pointer-table GEMV the reference adds (kernels/moe-cache.cu:76-291) is the
+// MUL_MAT_ID part.  For batch-1 decode every launch boundary costs microseconds
+// of dispatch and drain against a few microseconds of HBM time, so these two
+// kernels cover the whole block in two launches, with the GEMV steps of
+// mc_step.h unchanged:
+//
+//   mc_ffn_gate_up_kernel      (FFN_GATE_UP_NORM)
+//     workgroups of up to 8 step waves, one GEMV step (gate+up rows of one pick,
+//     or of the shared expert) per wave, and 4 prologue waves.  While the steps'
+//     weight spans stream into LDS, the prologue waves compute
+//     y = q8_1((x * s) * nw), s = 1/sqrt(mean(x^2) + eps) in the canonical RMS
+//     order (mc_internal.h), from the fp32 residual row x, and every step wave's
+//     dots read that row.  Bit-identical to the combine kernel's y followed by the
+//     q8_1 GEMV.
+//
+//   mc_ffn_down_combine_kernel (FFN_DOWN_COMBINE)
+//     one workgroup per (token, block of rows): wave c computes the rows of pick
+//     c's down projection (wave n_used: the shared expert), the results meet in
+//     LDS, and wave 0 writes x_out = residual + shared + sum_c w_c * o_c
+//     (fmaf, c ascending) -- the combine kernel's arithmetic, without o in HBM.
+//
+// A plain __syncthreads() would wait for every LDS-writing DMA of the wave
+// (its release fence drains them); lds_barrier() waits for LDS operations only,
+// and the gate/up kernel hands the normalized row to its step waves through LDS
+// counters instead of a barrier.
+#include <hip/hip_runtime.h>
+
+#include "mc_core.h"
+#include "mc_internal.h"
+#include "mc_step.h"
+
+namespace mc {
+
+// Workgroup barrier for data exchanged through LDS by ordinary LDS writes;
+// weight DMAs still in flight are not waited for.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// ---------------------------------------------------------------------------
+// gate/up with the RMSNorm + q8_1 prologue
+// ---------------------------------------------------------------------------
+
+// Waits (bounded) until the LDS counter reaches n; false on timeout.  The LDS reads
+// a wave issues afterwards are ordered after this read by the LDS unit.
+__device__ __forceinline__ bool wait_lds_count(const u32 *cnt, u32 n) {
+    for (int it = 0; it < (1 << 22); ++it) {
+        if (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= n) return true;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return false;
+}
+
+// A prologue wave p of token t handles chunks j = p + NP * ci, ci < PC: loads them
+// (x and the norm weights, into registers; an index past the row is clamped to the
+// last chunk, whose results it then rewrites with identical bytes, so loads,
+// arithmetic and stores are branch-free and the chunks' divisions interleave),
+// counts itself in sync[2] once the loads are issued (the step waves hold their
+// weight DMA until then, so these loads are not queued behind the weight stream),
+// publishes the chunks' canonical sums and counts them in sync[0], waits for the
+// other prologue waves' sums, and writes q8_1((x * scale) * nw) of its chunks to the
+// LDS row (and to y_out when asked), counted in sync[1].
+template <int PC>
+__device__ __forceinline__ void gu_prologue(const GemvArgs &a, int t, int p, float *red, uint8_t *ys, u32 *sync,
+                                            bool write_y_out) {
+    constexpr int NP = FFN_GU_PRO_WAVES;
+    const int lane = threadIdx.x % WAVE;
+    const int K = a.ncols, nchunk = K / RMS_CHUNK;
+    const float *xr = a.nx + (int64_t) t * a.nx_stride;
+    v4f xv[PC], nwv[PC];
+#pragma unroll
+    for (int ci = 0; ci < PC; ++ci) {
+        const int j = min(p + NP * ci, nchunk - 1);
+        xv[ci] = *(const v4f *) (xr + RMS_CHUNK * j + 4 * lane);
+        nwv[ci] = a.nw ? *(const v4f *) (a.nw + RMS_CHUNK * j + 4 * lane) : v4f{1.0f, 1.0f, 1.0f, 1.0f};
+    }
+    if (lane == 0) __hip_atomic_fetch_add(sync + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    float cs[PC];
+#pragma unroll
+    for (int ci = 0; ci < PC; ++ci) {
+        const float x4[4] = {xv[ci].x, xv[ci].y, xv[ci].z, xv[ci].w};
+        cs[ci] = rms_chunk_sum(x4);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int ci = 0; ci < PC; ++ci) red[min(p + NP * ci, nchunk - 1)] = cs[ci];
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");      // the sums are in LDS before the count
+    if (lane == 0) __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    wait_lds_count(sync, (u32) NP);
+    float ss = 0.0f;                                          // ascending, as every other producer of y
+    for (int j = 0; j < nchunk; ++j) ss += red[j];
+    const float scale = 1.0f / sqrtf(ss / (float) K + a.eps);
+#pragma unroll
+    for (int ci = 0; ci < PC; ++ci) {
+        const float x4[4] = {xv[ci].x, xv[ci].y, xv[ci].z, xv[ci].w};
+        quantize_chunk<false>(x4, true, scale, nwv[ci], ys, min(p + NP * ci, nchunk - 1));
+    }
+    if (write_y_out) {
+#pragma unroll
+        for (int ci = 0; ci < PC; ++ci) {
+            const float x4[4] = {xv[ci].x, xv[ci].y, xv[ci].z, xv[ci].w};
+            quantize_chunk<true>(x4, true, scale, nwv[ci], a.y_out + (int64_t) t * a.y_out_stride,
+                                 min(p + NP * ci, nchunk - 1));
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");      // the row is in LDS before the count
+    if (lane == 0) __hip_atomic_fetch_add(sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Workgroup: FFN_GU_PRO_WAVES prologue waves, then nwaves step waves (one GEMV step
+// each).  The step waves issue their weight spans first and only wait for the
+// normalized row once their gate span has landed; no workgroup barrier follows the
+// start, so no wave waits for another wave's weight stream.
+// Dynamic LDS: [nwaves x (up span | gate span)] [q8_1 row] [2 counters | chunk sums]
+template <int TW, int TS>
+__global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void mc_ffn_gate_up_kernel(const GemvArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr int NP = FFN_GU_PRO_WAVES;
+    // the wave index is uniform across the wave: keep it (and the step) in scalar registers
+    const int wave = __builtin_amdgcn_readfirstlane((int) (threadIdx.x / WAVE));
+    if (a.rec && blockIdx.x == 0) {
+        if (wave == 0) record_picks(a);
+        return;
+    }
+    const int b = (int) blockIdx.x - a.rec;
+    const int t = b / a.wg_per_tok;
+    uint8_t *ys = lds + a.lds_y;
+    u32 *sync = (u32 *) (lds + a.lds_part);
+    float *red = (float *) (lds + a.lds_part + 16);
+    if (threadIdx.x == 0) {
+        sync[0] = 0u;
+        sync[1] = 0u;
+        sync[2] = 0u;
+    }
+    lds_barrier();                                            // counters set; nothing is in flight yet
+    if (wave < NP) {
+        const bool y_out = a.y_out && (b % a.wg_per_tok) == 0;
+        if (a.ncols <= 4 * NP * RMS_CHUNK) gu_prologue<4>(a, t, wave, red, ys, sync, y_out);
+        else gu_prologue<8192 / RMS_CHUNK / NP>(a, t, wave, red, ys, sync, y_out);
+        return;
+    }
+    const int sw = wave - NP;
+    const int local = (b % a.wg_per_tok) * a.nwaves + sw;      // this wave's step within token t
+    uint8_t *span = lds + (u32) sw * a.lds_wave;
+    const bool has_step = local < a.tiles_per_tok;
+    const bool sh = local < a.sh_tiles_per_tok;
+    if (!has_step) return;
+    if constexpr (TS == 0) {
+        if (sh) return;                                       // no shared tiles without a shared type
+    }
+    StepCtx s = sh ? step_locate(a, true, t * a.sh_tiles_per_tok + local)
+                   : step_locate(a, false, t * a.n_used * a.tiles_per_pick + (local - a.sh_tiles_per_tok));
+    step_resolve(a, s);
+    if (!s.valid) return;
+    wait_lds_count(sync + 2, (u32) NP);                       // the prologue's loads go out first
+    if (sh) {
+        if constexpr (TS != 0) step_dma<TS>(a, s, span);
+    } else {
+        step_dma<TW>(a, s, span);
+    }
+    wait_loads_at_most(s.wgate ? s.n_up : 0);                 // gate span landed (up may still land)
+    if (!wait_lds_count(sync + 1, (u32) NP)) return;          // the normalized row is complete
+    float su, sg;
+    if (sh) {
+        if constexpr (TS != 0) {
+            step_dots<TS, ACT_Q8_1>(a, s, span, ys, su, sg);
+            step_store<TS>(a, s, su, sg);
+        }
+    } else {
+        step_dots<TW, ACT_Q8_1>(a, s, span, ys, su, sg);
+        step_store<TW>(a, s, su, sg);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// down projection + combine
+// ---------------------------------------------------------------------------
+// Dynamic LDS: [nwaves x (span | activation staging | q8_1 row)] [row results nwaves x rps]
+template <int TW, int TS, int ACT>
+__global__ __launch_bounds__(FFN_DN_MAX_WAVES *WAVE) void mc_ffn_down_combine_kernel(const GemvArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr int AQ = ACT == ACT_F32 ? ACT_Q8_1 : ACT;
+    const int wave = __builtin_amdgcn_readfirstlane((int) (threadIdx.x / WAVE)), lane = threadIdx.x % WAVE;
+    if (a.rec && blockIdx.x == 0) {
+        if (wave == 0) record_picks(a);
+        return;
+    }
+    const int b = (int) blockIdx.x - a.rec;
+    const int t = b / a.wg_per_tok;
+    const int rt = b % a.wg_per_tok;                    // row tile
+    const bool sh = wave == a.n_used;                   // the shared expert's wave
+    uint8_t *span = lds + (u32) wave * a.lds_wave;
+    float *part = (float *) (lds + a.lds_part);         // [nwaves][rps]
+    const int rps = a.rps;
+
+    StepCtx s = sh ? step_locate(a, true, t * a.sh_tiles_per_tok + rt)
+                   : step_locate(a, false, (t * a.n_used + wave) * a.tiles_per_pick + rt);
+    // activation row of the wave's pick (or of the shared expert), first
+    const uint8_t *ybase;
+    u32 yrow, ybytes;
+    if (!sh) {
+        ybase = a.y;
+        ybytes = (u32) a.y_bytes;
+        yrow = (u32) ((int64_t) (s.c % (int) a.nchannels_y) * a.stride_channel_y + (int64_t) s.t * a.stride_col_y);
+    } else {
+        ybase = a.sh_y;
+        ybytes = (u32) a.sh_y_bytes;
+        yrow = (u32) ((int64_t) s.t * a.sh_stride_col_y);
+    }
+    const u32 alead = dma_bytes(ybase, ybytes, yrow, a.act_row_bytes, span + a.lds_act);
+    if (sh) {
+        if constexpr (TS != 0) step_issue<TS>(a, s, span);
+    } else {
+        step_issue<TW>(a, s, span);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    float v = 0.0f;                                     // an out-of-range expert id contributes 0
+    int nu = 1;
+    if (s.valid) {
+        const uint8_t *arow = span + a.lds_act + alead;
+        if constexpr (ACT == ACT_F32) {
+            quantize_row_lds((const float *) arow, span + a.lds_q8, a.ncols);
+            arow = span + a.lds_q8;
+        }
+        float su = 0.0f, sg = 0.0f;
+        if (sh) {
+            if constexpr (TS != 0) {
+                step_dots<TS, AQ>(a, s, span, arow, su, sg);
+                nu = a.ncols / type_geom(TS).unit_elems;
+            }
+            v = su;
+        } else {
+            step_dots<TW, AQ>(a, s, span, arow, su, sg);
+            nu = a.ncols / type_geom(TW).unit_elems;
+            const int rl = lane / nu;
+            v = routed_value(a, s, s.row0 + (rl < s.nrows_here ? rl : 0), su, sg);
+        }
+    }
+    {
+        const int rl = lane / nu;
+        if (s.valid) {
+            if (lane % nu == 0 && rl < s.nrows_here) part[wave * rps + rl] = v;
+        } else if (lane < s.nrows_here) {
+            part[wave * rps + lane] = 0.0f;
+        }
+    }
+    lds_barrier();
+    // x = residual + shared + sum_c w_c * o_c, one lane per row
+    if (wave == 0 && lane < s.nrows_here) {
+        const int row = s.row0 + lane;
+        float x = a.residual ? a.residual[(int64_t) t * a.x_stride + row] : 0.0f;
+        if (a.nwaves > a.n_used) x += part[a.n_used * rps + lane];
+        const float *w = a.router_w + (int64_t) t * a.n_used;
+        for (int c = 0; c < a.n_used; ++c) x = fmaf(w[c], part[c * rps + lane], x);
+        a.x_out[(int64_t) t * a.x_stride + row] = x;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+
+template <class K>
+static hipError_t launch_big_lds(K kernel, unsigned grid, unsigned block, uint32_t lds, const GemvArgs &a, hipStream_t s) {
+    static_cast<void>(hipFuncSetAttribute((const void *) kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int) FFN_LDS_MAX));
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(block), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int TW, int TS>
+static hipError_t launch_gu_t(const GemvArgs &a, hipStream_t s) {
+    return launch_big_lds(mc_ffn_gate_up_kernel<TW, TS>, (unsigned) (a.rec + a.n_tok * a.wg_per_tok),
+                          (unsigned) ((a.nwaves + FFN_GU_PRO_WAVES) * WAVE), a.lds_total, a, s);
+}
+
+template <int TW, int TS, int ACT>
+static hipError_t launch_dn_t(const GemvArgs &a, hipStream_t s) {
+    return launch_big_lds(mc_ffn_down_combine_kernel<TW, TS, ACT>, (unsigned) (a.rec + a.n_tok * a.wg_per_tok),
+                          (unsigned) (a.nwaves * WAVE), a.lds_total, a, s);
+}
+
+template <int TW, int TS>
+static hipError_t launch_mode(const GemvArgs &a, int act, hipStream_t s) {
+    if (a.mode == FFN_GATE_UP_NORM) return launch_gu_t<TW, TS>(a, s);
+    if (act == ACT_F32) return launch_dn_t<TW, TS, ACT_F32>(a, s);
+    return launch_dn_t<TW, TS, ACT_Q8_1>(a, s);
+}
+
+template <int TW>
+static hipError_t launch_ts(const GemvArgs &a, int ts, int act, hipStream_t s) {
+    switch (ts) {
+        case 0: return launch_mode<TW, 0>(a, act, s);
+        case T_Q2_K: return launch_mode<TW, T_Q2_K>(a, act, s);
+        case T_Q3_K: return launch_mode<TW, T_Q3_K>(a, act, s);
+        case T_Q4_K: return launch_mode<TW, T_Q4_K>(a, act, s);
+        case T_Q5_K: return launch_mode<TW, T_Q5_K>(a, act, s);
+        case T_Q6_K: return launch_mode<TW, T_Q6_K>(a, act, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+static uint32_t round16(uint32_t b) { return (b + 15u) & ~15u; }
+
+// Tiling and LDS layout of the fused kernels; returns hipErrorInvalidValue when
+// the shape does not fit (the host validated types and alignment).
+static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act) {
+    const TypeGeom g = type_geom(tw);
+    const int nu = a.ncols / g.unit_elems;
+    const uint32_t rb = (uint32_t) nu * (uint32_t) g.unit_bytes;
+    const int nus = ts ? a.ncols / type_geom(ts).unit_elems : 1;
+    const uint32_t rbs = ts ? (uint32_t) nus * (uint32_t) type_geom(ts).unit_bytes : 0u;
+    const int nspan = a.has_gate || (ts && a.sh_gate) ? 2 : 1;
+    a.rec = (a.stats || a.stamps || a.stamps_gate) ? 1 : 0;
+    if (a.mode == FFN_GATE_UP_NORM) {
+        if (a.ncols % RMS_CHUNK || a.ncols > 8192) return hipErrorInvalidValue;
+        const uint32_t common = round16((uint32_t) (a.ncols / 32 * 36)) + 16u + 4u * (uint32_t) (a.ncols / RMS_CHUNK);
+        int rps = WAVE / nu, sh_rps = ts ? WAVE / nus : 0;
+        for (;;) {
+            a.tiles_per_pick = (a.nrows + rps - 1) / rps;
+            a.sh_tiles_per_tok = ts ? (a.nrows + sh_rps - 1) / sh_rps : 0;
+            a.tiles_per_tok = a.sh_tiles_per_tok + a.n_used * a.tiles_per_pick;
+            // as many waves per workgroup as fill about one workgroup per CU
+            const int want = (a.tiles_per_tok * a.n_tok + 255) / 256;
+            a.nwaves = want < 1 ? 1 : (want > FFN_GU_MAX_WAVES ? FFN_GU_MAX_WAVES : want);
+            const uint32_t sr = span_bytes((uint32_t) rps, rb);
+            const uint32_t ss = ts ? span_bytes((uint32_t) sh_rps, rbs) : 0u;
+            a.lds_span = sr > ss ? sr : ss;
+            a.lds_wave = (uint32_t) nspan * a.lds_span;
+            if ((uint32_t) a.nwaves * a.lds_wave + common <= FFN_LDS_MAX) break;
+            if (ts && ss >= sr && sh_rps > 1) --sh_rps;
+            else if (rps > 1) --rps;
+            else return hipErrorInvalidValue;
+        }
+        a.rps = rps;
+        a.sh_rps = sh_rps;
+        a.wg_per_tok = (a.tiles_per_tok + a.nwaves - 1) / a.nwaves;
+        a.lds_y = (uint32_t) a.nwaves * a.lds_wave;
+        a.lds_part = a.lds_y + round16((uint32_t) (a.ncols / 32 * 36));
+        a.lds_total = a.lds_part + 16u + 4u * (uint32_t) (a.ncols / RMS_CHUNK);
+        a.n_tiles = a.tiles_per_tok * a.n_tok;
+        return hipSuccess;
+    }
+    // FFN_DOWN_COMBINE: one wave per pick (+ the shared expert), common rows per step
+    a.nwaves = a.n_used + (ts ? 1 : 0);
+    if (a.nwaves > FFN_DN_MAX_WAVES || nspan != 1) return hipErrorInvalidValue;
+    int rps = WAVE / nu;
+    if (ts && WAVE / nus < rps) rps = WAVE / nus;
+    // enough workgroups for every CU: at most nrows * n_tok / 256 rows each
+    const int fill = (a.nrows * a.n_tok + 255) / 256;
+    if (fill < rps) rps = fill < 1 ? 1 : fill;
+    const uint32_t q8_bytes = act == ACT_F32 ? round16((uint32_t) (a.ncols / 32 * 36)) : 0u;
+    for (;;) {
+        const uint32_t sr = span_bytes((uint32_t) rps, rb);
+        const uint32_t ss = ts ? span_bytes((uint32_t) rps, rbs) : 0u;
+        a.lds_span = sr > ss ? sr : ss;
+        a.lds_act = a.lds_span;
+        a.lds_q8 = a.lds_act + round_up_1k(a.act_row_bytes + 20u);
+        a.lds_wave = a.lds_q8 + q8_bytes;
+        a.lds_part = (uint32_t) a.nwaves * a.lds_wave;
+        a.lds_total = a.lds_part + 4u * (uint32_t) (a.nwaves * rps);
+        if (a.lds_total <= FFN_LDS_MAX) break;
+        if (rps > 1) --rps;
+        else return hipErrorInvalidValue;
+    }
+    a.rps = rps;
+    a.sh_rps = rps;
+    a.tiles_per_pick = (a.nrows + rps - 1) / rps;
+    a.sh_tiles_per_tok = ts ? a.tiles_per_pick : 0;
+    a.wg_per_tok = a.tiles_per_pick;
+    a.tiles_per_tok = a.wg_per_tok;
+    a.n_tiles = a.wg_per_tok * a.n_tok;
+    return hipSuccess;
+}
+
+// Fused decode launch (a.mode != FFN_NONE): tiling, LDS layout, dispatch on the
+// routed type (K-quants) and the shared-expert type (none or a K-quant).
+int launch_ffn(GemvArgs a, int tw, int ts, int act, void *stream) {
+    if (ts == 0 || !a.sh_up) ts = 0;
+    if (a.mode == FFN_GATE_UP_NORM) act = ACT_Q8_1;
+    a.act_row_bytes = act == ACT_Q8_1 ? (uint32_t) (a.ncols / 32 * 36) : (uint32_t) a.ncols * 4u;
+    hipError_t err = ffn_layout(a, tw, ts, act);
+    if (err != hipSuccess) return (int) err;
+    if (a.n_tiles <= 0) return (int) hipSuccess;
+    hipStream_t s = (hipStream_t) stream;
+    switch (tw) {
+        case T_Q2_K: return (int) launch_ts<T_Q2_K>(a, ts, act, s);
+        case T_Q3_K: return (int) launch_ts<T_Q3_K>(a, ts, act, s);
+        case T_Q4_K: return (int) launch_ts<T_Q4_K>(a, ts, act, s);
+        case T_Q5_K: return (int) launch_ts<T_Q5_K>(a, ts, act, s);
+        case T_Q6_K: return (int) launch_ts<T_Q6_K>(a, ts, act, s);
+        default: return (int) hipErrorInvalidValue;
+    }
+}
+
+}  // namespace mc

@@ -480,12 +480,28 @@ bool wants_impl(const ggml_hip_moe_tensor *src0) {
     return is_contiguous(src0);
 }
 
-// Shared validation + launch of the GEMV.
+// Inputs of the fused decode kernels (GemvArgs fields of the same names).
+struct FfnExtra {
+    int mode = FFN_NONE;
+    const float *nx = nullptr;
+    int64_t nx_stride = 0;
+    const float *nw = nullptr;
+    float eps = 0.0f;
+    uint8_t *y_out = nullptr;
+    int64_t y_out_stride = 0;
+    const float *router_w = nullptr;
+    const float *residual = nullptr;
+    float *x_out = nullptr;
+    int64_t x_stride = 0;
+};
+
+// Shared validation + launch of the GEMV (and of the fused decode kernels when fx is given).
 int gemv_common(int use_cache, int act, const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *gate_host,
                 const ggml_hip_moe_fusion *fusion, const void *src1, const int32_t *ids_d, float *dst_d,
                 int64_t ne00, int64_t ne01, int64_t ne02, int64_t ncols_dst, int64_t nchannels_y, int64_t nchannels_dst,
                 int64_t stride_col_y, int64_t stride_col_dst, int64_t stride_channel_y, int64_t stride_channel_dst,
-                int64_t ids_stride, void *stream) {
+                int64_t ids_stride, void *stream, const FfnExtra *fx = nullptr) {
+    const int mode = fx ? fx->mode : FFN_NONE;
     if (!src0 || !src1 || !ids_d || !dst_d) return fail(E_INVALID, "moe-gemv: null argument");
     const int tw = src0->type;
     if (!type_supported(tw)) return fail(E_UNSUPPORTED, "moe-gemv: unsupported expert type %d", tw);
@@ -512,7 +528,12 @@ int gemv_common(int use_cache, int act, const ggml_hip_moe_tensor *src0, const g
         if (ne00 % type_geom(ts).unit_elems || ne00 / type_geom(ts).unit_elems > WAVE)
             return fail(E_UNSUPPORTED, "moe-gemv: shared-expert row length not supported");
         if (act == ACT_Q8_K && !type_geom(ts).kquant) return fail(E_UNSUPPORTED, "moe-gemv: q8_K activations need a K-quant shared expert");
-        if (!fusion->shared_dst) return fail(E_INVALID, "moe-gemv: shared_up without shared_dst");
+        if (!fusion->shared_dst && mode != FFN_DOWN_COMBINE) return fail(E_INVALID, "moe-gemv: shared_up without shared_dst");
+    }
+    if (mode != FFN_NONE) {
+        // the fused decode kernels are built for K-quant experts (and K-quant shared experts)
+        if (!g.kquant || (ts && !type_geom(ts).kquant))
+            return fail(E_UNSUPPORTED, "moe-ffn: fused decode kernels take K-quant experts (type %d, shared %d)", tw, ts);
     }
     const bool aligned_ok = g.aligned ? ((((uintptr_t) src0->data) | eb) & 3u) == 0 : ((((uintptr_t) src0->data) | eb) & 1u) == 0;
     if (!aligned_ok) return fail(E_UNSUPPORTED, "moe-gemv: expert base/size alignment not supported");
@@ -611,7 +632,26 @@ int gemv_common(int use_cache, int act, const ggml_hip_moe_tensor *src0, const g
         a.tbl_gate = r->d_tbl;
         a.has_gate = 1;
     }
-    if ((rc = dev()->launch_gemv(a, tw, ts, act, stream))) return dev_err(rc, "GEMV launch");
+    if (!use_cache) {
+        // every expert is device memory at a fixed stride: the kernel computes the
+        // address instead of reading the (identical) resident table entry
+        a.w_base = (const uint8_t *) src0->data;
+        a.w_gate_base = a.has_gate ? (const uint8_t *) fusion->gate : nullptr;
+    }
+    if (fx) {
+        a.mode = fx->mode;
+        a.nx = fx->nx;
+        a.nx_stride = fx->nx_stride;
+        a.nw = fx->nw;
+        a.eps = fx->eps;
+        a.y_out = fx->y_out;
+        a.y_out_stride = fx->y_out_stride;
+        a.router_w = fx->router_w;
+        a.residual = fx->residual;
+        a.x_out = fx->x_out;
+        a.x_stride = fx->x_stride;
+    }
+    if ((rc = dev()->launch_gemv(a, tw, ts, act, stream))) return dev_err(rc, mode == FFN_NONE ? "GEMV launch" : "fused FFN launch");
     return 0;
 }
 
@@ -690,6 +730,60 @@ int ggml_hip_moe_mul_mat_vec_ex(int use_cache, int act_format, const ggml_hip_mo
     return gemv_common(use_cache ? 1 : 0, act_format, src0, gate_host, fusion, src1, ids_d, dst_d, ne00, ne01, ne02, ncols_dst,
                        nchannels_y, nchannels_dst, stride_col_y, stride_col_dst, stride_channel_y, stride_channel_dst,
                        ids_stride, stream);
+}
+
+int ggml_hip_moe_ffn_gate_up_norm(int use_cache, const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *gate_host,
+                                  const ggml_hip_moe_fusion *fusion, const float *x, const float *norm_weight, float eps,
+                                  const int32_t *ids_d, float *dst_d, int64_t ne00, int64_t ne01, int64_t ne02,
+                                  int64_t ncols_dst, int64_t nchannels_dst, int64_t stride_col_x, int64_t stride_col_dst,
+                                  int64_t stride_channel_dst, int64_t ids_stride, void *y_out, int64_t y_out_stride,
+                                  void *stream) {
+    if (!x) return fail(E_INVALID, "moe-ffn: null x");
+    if (use_cache && !wants_impl(src0)) return fail(E_STATE, "moe-cache: src0 does not qualify for the cache path (wants() == 0)");
+    if (!use_cache && gate_host) return fail(E_INVALID, "moe-gemv: gate_host is for the cache path; pass fusion->gate");
+    if (ne00 <= 0 || ne00 % 256 || ne00 > 8192) return fail(E_UNSUPPORTED, "moe-ffn: ne00=%lld must be a multiple of 256 up to 8192", (long long) ne00);
+    if ((((uintptr_t) x) & 15u) || (stride_col_x & 3) || (ncols_dst > 1 && stride_col_x < ne00))
+        return fail(E_INVALID, "moe-ffn: x rows must be 16-byte aligned and not overlap");
+    if (norm_weight && (((uintptr_t) norm_weight) & 15u)) return fail(E_INVALID, "moe-ffn: norm_weight must be 16-byte aligned");
+    if (y_out && ((((uintptr_t) y_out) & 3u) || (ncols_dst > 1 && y_out_stride < ne00 / 32)))
+        return fail(E_INVALID, "moe-ffn: y_out rows must be 4-byte aligned and not overlap");
+    if (fusion && fusion->shared_src1) return fail(E_INVALID, "moe-ffn: the shared expert reads the normalized row (shared_src1 must be NULL)");
+    FfnExtra fx;
+    fx.mode = FFN_GATE_UP_NORM;
+    fx.nx = x;
+    fx.nx_stride = stride_col_x;
+    fx.nw = norm_weight;
+    fx.eps = eps;
+    fx.y_out = (uint8_t *) y_out;
+    fx.y_out_stride = y_out_stride * 36;
+    // the dots read the q8_1 row built in LDS; src1 stands in for the activation argument
+    return gemv_common(use_cache ? 1 : 0, ACT_Q8_1, src0, gate_host, fusion, x, ids_d, dst_d, ne00, ne01, ne02, ncols_dst,
+                       1, nchannels_dst, 0, stride_col_dst, 0, stride_channel_dst, ids_stride, stream, &fx);
+}
+
+int ggml_hip_moe_ffn_down_combine(int use_cache, int act_format, const ggml_hip_moe_tensor *src0,
+                                  const ggml_hip_moe_fusion *fusion, const void *src1, const int32_t *ids_d,
+                                  const float *router_w, const float *residual, float *x_out, int64_t ne00, int64_t ne01,
+                                  int64_t ne02, int64_t ncols_dst, int64_t nchannels_dst, int64_t stride_col_y,
+                                  int64_t stride_channel_y, int64_t stride_col_x, int64_t ids_stride, void *stream) {
+    if (!router_w || !x_out) return fail(E_INVALID, "moe-ffn: null router weights or x_out");
+    if (use_cache && !wants_impl(src0)) return fail(E_STATE, "moe-cache: src0 does not qualify for the cache path (wants() == 0)");
+    if (act_format != ACT_Q8_1 && act_format != ACT_F32) return fail(E_UNSUPPORTED, "moe-ffn: down activations are q8_1 or fp32 rows");
+    if (fusion && (fusion->gate || fusion->shared_gate || fusion->gate_bias || fusion->gate_scale))
+        return fail(E_INVALID, "moe-ffn: the down projection takes no gate");
+    if (fusion && fusion->shared_up && !fusion->shared_src1) return fail(E_INVALID, "moe-ffn: shared expert without its activation row (shared_src1)");
+    if (stride_col_x < ne01 && ncols_dst > 1) return fail(E_INVALID, "moe-ffn: x rows overlap");
+    if ((((uintptr_t) x_out) | ((uintptr_t) residual) | ((uintptr_t) router_w)) & 3u) return fail(E_INVALID, "moe-ffn: misaligned fp32 buffers");
+    FfnExtra fx;
+    fx.mode = FFN_DOWN_COMBINE;
+    fx.router_w = router_w;
+    fx.residual = residual;
+    fx.x_out = x_out;
+    fx.x_stride = stride_col_x;
+    // dst strides only set the default per-expert bias stride (ne01); the kernel writes x_out
+    return gemv_common(use_cache ? 1 : 0, act_format, src0, nullptr, fusion, src1, ids_d, x_out, ne00, ne01, ne02, ncols_dst,
+                       nchannels_dst, nchannels_dst, stride_col_y, ne01 * nchannels_dst, stride_channel_y, ne01, ids_stride,
+                       stream, &fx);
 }
 
 int ggml_hip_moe_cache_step(void *stream) {

@@ -77,6 +77,10 @@ struct GemvArgs {
     int32_t n_experts;
     int32_t has_gate;             // 1: fused gate present (through tbl_gate)
     uint64_t expert_bytes;        // bytes of one expert matrix
+    // device-resident tensors: expert e at w_base + e * expert_bytes (no table
+    // read on the way to the weights); null: resolve through tbl / tbl_gate
+    const uint8_t *w_base;
+    const uint8_t *w_gate_base;
     // activations
     const uint8_t *y;             // activation base (q8_1 or q8_K blocks)
     uint64_t y_bytes;             // addressable bytes from y (buffer range)
@@ -125,7 +129,33 @@ struct GemvArgs {
     uint32_t lds_q8;              // LDS offset of the in-kernel q8_1 copy of an fp32 activation row
     uint32_t lds_red;             // LDS offset of the 64-float reduction scratch
     uint32_t lds_total;           // dynamic LDS bytes per workgroup
+    // fused decode kernels (mc_ffn.hip); FFN_NONE: the plain MUL_MAT_ID GEMV
+    int32_t mode;
+    int32_t nwaves;               // step waves per workgroup (FFN_GATE_UP_NORM: plus FFN_GU_PRO_WAVES)
+    int32_t wg_per_tok;           // workgroups per token
+    int32_t tiles_per_tok;        // steps per token: shared tiles first, then the routed picks'
+    uint32_t lds_wave;            // LDS bytes of one wave's region (spans, activation staging)
+    uint32_t lds_y;               // FFN_GATE_UP_NORM: q8_1 row
+    uint32_t lds_part;            // FFN_GATE_UP_NORM: counters + chunk sums; FFN_DOWN_COMBINE: row results [nwaves][rps]
+    // FFN_GATE_UP_NORM: y = q8_1((x * rms_scale(x)) * nw), computed by every workgroup
+    const float *nx;              // [n_tok][nx_stride] rows to normalize
+    int64_t nx_stride;            // floats
+    const float *nw;              // [ncols] norm weight, or null
+    float eps;
+    uint8_t *y_out;               // optional copy of the q8_1 rows (written by each token's first workgroup)
+    int64_t y_out_stride;         // bytes
+    // FFN_DOWN_COMBINE: x_out = residual + shared + sum_c router_w[c] * o_c (c ascending, fmaf)
+    const float *router_w;        // [n_tok][n_used]
+    const float *residual;        // [n_tok][x_stride], or null
+    float *x_out;                 // [n_tok][x_stride]
+    int64_t x_stride;             // floats
 };
+
+enum : int { FFN_NONE = 0, FFN_GATE_UP_NORM = 1, FFN_DOWN_COMBINE = 2 };
+constexpr int FFN_GU_MAX_WAVES = 8;    // gate/up workgroups: up to 8 step waves sharing one normalized row
+constexpr int FFN_GU_PRO_WAVES = 4;    // ... plus 4 waves that compute that row (no weight DMA of their own)
+constexpr int FFN_DN_MAX_WAVES = 12;   // down + combine workgroups: one wave per pick + the shared expert
+constexpr uint32_t FFN_LDS_MAX = 160 * 1024;
 
 // LDS a GEMV workgroup may use, chosen so that 8 workgroups fit one CU's
 // 160 KiB: a decode launch of ~2000 single-wave tiles is then resident at once.

@@ -25,179 +25,50 @@
 
 #include "mc_core.h"
 #include "mc_internal.h"
+#include "mc_step.h"
 
 namespace mc {
 
 // ---------------------------------------------------------------------------
-// pick recorder (workgroup 0): stamps, hit count, canonical miss log
-// ---------------------------------------------------------------------------
-
-__device__ void record_picks(const GemvArgs &a) {
-    const int lane = threadIdx.x;
-    const int n_picks = a.n_tok * a.n_used;
-    const u32 clk = a.clock ? *a.clock : 0u;
-    for (int p0 = 0; p0 < n_picks; p0 += WAVE) {
-        const int p = p0 + lane;
-        int e = -1;
-        u32 miss_up = 0, miss_gate = 0, hits = 0;
-        if (p < n_picks) {
-            const int t = p / a.n_used, c = p % a.n_used;
-            e = a.ids[c + (int64_t) t * a.ids_stride];
-            if (e >= 0 && e < a.n_experts) {
-                const uint64_t pu = a.tbl[e];
-                if (a.stamps) a.stamps[e] = clk;
-                miss_up = (u32) (pu & 1u);
-                hits += 1u - miss_up;
-                if (a.tbl_gate) {
-                    const uint64_t pg = a.tbl_gate[e];
-                    if (a.stamps_gate) a.stamps_gate[e] = clk;
-                    miss_gate = (u32) (pg & 1u);
-                    hits += 1u - miss_gate;
-                }
-            }
-        }
-        if (!a.stats) continue;
-        // exclusive prefix sum of miss counts across the wave (pick order)
-        const u32 nm = miss_up + miss_gate;
-        u32 incl = nm;
-#pragma unroll
-        for (int off = 1; off < WAVE; off <<= 1) {
-            const u32 v = (u32) __shfl_up((int) incl, off, WAVE);
-            if (lane >= off) incl += v;
-        }
-        const u32 total = (u32) __shfl((int) incl, WAVE - 1, WAVE);
-        u32 hsum = hits;
-#pragma unroll
-        for (int off = WAVE / 2; off > 0; off >>= 1) hsum += (u32) __shfl_xor((int) hsum, off, WAVE);
-        u32 start = 0;
-        if (lane == 0) {
-            start = atomicAdd(a.stats, total);
-            if (hsum) atomicAdd(a.stats + HIT_WORD, hsum);
-        }
-        start = (u32) __shfl((int) start, 0, WAVE);
-        const u32 pos = start + incl - nm;
-        if (miss_up && pos < (u32) MISS_CAP) a.stats[LOG_BASE + pos] = ((u32) a.cache_id << 12) | (u32) e;
-        if (miss_gate && pos + miss_up < (u32) MISS_CAP)
-            a.stats[LOG_BASE + pos + miss_up] = ((u32) a.cache_id_gate << 12) | (u32) e;
-    }
-}
-
-// ---------------------------------------------------------------------------
-// one step of one matrix pair (up [+ gate]) for one pick
+// one step of one matrix pair (up [+ gate]) for one pick (mc_step.h)
 // ---------------------------------------------------------------------------
 template <int T, int ACT>
 __device__ __forceinline__ void run_step(const GemvArgs &a, uint8_t *lds, bool shared, int tile) {
-    constexpr TypeGeom G = type_geom(T);
-    constexpr int UE = G.unit_elems, UB = G.unit_bytes;
     constexpr int AQ = ACT == ACT_F32 ? ACT_Q8_1 : ACT;          // block format the dots read
-    constexpr int AUB = AQ == ACT_Q8_1 ? UE / 32 * 36 : 292;     // activation bytes per unit
-    const int lane = threadIdx.x;
-    const int K = a.ncols;
-    const int nu = K / UE;                   // units per row (<= 64, checked on the host)
-    const int rps = shared ? a.sh_rps : a.rps;
-    const u32 RB = (u32) nu * UB;            // row bytes
-
+    StepCtx s = step_locate(a, shared, tile);
     // the activation row depends only on (token, slot): its DMA goes out first
-    int t, c = 0, row0, pick = 0;
     const uint8_t *ybase;
     u32 yrow, ybytes;
     if (!shared) {
-        pick = tile / a.tiles_per_pick;
-        row0 = (tile % a.tiles_per_pick) * rps;
-        t = pick / a.n_used;
-        c = pick % a.n_used;
         ybase = a.y;
         ybytes = (u32) a.y_bytes;
-        yrow = (u32) ((int64_t) (c % (int) a.nchannels_y) * a.stride_channel_y + (int64_t) t * a.stride_col_y);
+        yrow = (u32) ((int64_t) (s.c % (int) a.nchannels_y) * a.stride_channel_y + (int64_t) s.t * a.stride_col_y);
+    } else if (a.sh_y) {
+        ybase = a.sh_y;
+        ybytes = (u32) a.sh_y_bytes;
+        yrow = (u32) ((int64_t) s.t * a.sh_stride_col_y);
     } else {
-        t = tile / a.sh_tiles_per_tok;
-        row0 = (tile % a.sh_tiles_per_tok) * rps;
-        if (a.sh_y) {
-            ybase = a.sh_y;
-            ybytes = (u32) a.sh_y_bytes;
-            yrow = (u32) ((int64_t) t * a.sh_stride_col_y);
-        } else {
-            ybase = a.y;
-            ybytes = (u32) a.y_bytes;
-            yrow = (u32) ((int64_t) t * a.stride_col_y);
-        }
+        ybase = a.y;
+        ybytes = (u32) a.y_bytes;
+        yrow = (u32) ((int64_t) s.t * a.stride_col_y);
     }
     const u32 alead = dma_bytes(ybase, ybytes, yrow, a.act_row_bytes, lds + a.lds_act);
-
-    // resolve the weights: expert id and tagged table entries through the scalar cache
-    int e = 0;
-    const uint8_t *wup, *wgate = nullptr;
-    u32 mbytes;
-    if (!shared) {
-        e = sload(a.ids + c + (int64_t) t * a.ids_stride);
-        if (e < 0 || e >= a.n_experts) {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            return;
-        }
-        wup = (const uint8_t *) (uintptr_t) (sload(a.tbl + e) & ~(uint64_t) 1);
-        if (a.has_gate) wgate = (const uint8_t *) (uintptr_t) (sload(a.tbl_gate + e) & ~(uint64_t) 1);
-        mbytes = (u32) a.expert_bytes;
-    } else {
-        wup = a.sh_up;
-        wgate = a.sh_gate;
-        mbytes = (u32) a.sh_matrix_bytes;
+    step_issue<T>(a, s, lds);
+    if (!s.valid) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        return;
     }
-    const int nrows_here = min(rps, a.nrows - row0);
-    const u32 start = (u32) row0 * RB, nbytes = (u32) nrows_here * RB;
-
-    // gate span, then up span; the gate dot runs while the up span is landing
-    if (wgate) dma_span<T>(wgate, mbytes, start, nbytes, lds + a.lds_span);
-    const int n_up = dma_span<T>(wup, mbytes, start, nbytes, lds);
-
-    const int row_local = lane / nu, col = lane % nu;
-    const bool active = row_local < nrows_here;
-    const int unit = row_local * nu + col;
-    // fp32 activations: the wave quantizes its staged row to q8_1 blocks in LDS
+    // activation and gate span landed (the gate dot then runs while the up span lands)
+    wait_loads_at_most(s.wgate ? s.n_up : 0);
     const uint8_t *arow = lds + a.lds_act + alead;
-    if constexpr (ACT == ACT_F32) arow = lds + a.lds_q8;
-    const uint8_t *aslice = arow + (u32) col * AUB;
-    Act<UE> A;
-    float pu = 0.0f, pg = 0.0f;
-    if (wgate) {
-        wait_loads_at_most(n_up);            // activation and gate span have landed
-        if constexpr (ACT == ACT_F32) quantize_row_lds((const float *) (lds + a.lds_act + alead), lds + a.lds_q8, K);
-        if (active) {
-            load_act_lds<UE, AQ>(A, aslice);
-            pg = span_unit_dot<T, AQ>(lds + a.lds_span, span_lead(wgate, start), unit, A);
-        }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        if (active) pu = span_unit_dot<T, AQ>(lds, span_lead(wup, start), unit, A);
-    } else {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        if constexpr (ACT == ACT_F32) quantize_row_lds((const float *) (lds + a.lds_act + alead), lds + a.lds_q8, K);
-        if (active) {
-            load_act_lds<UE, AQ>(A, aslice);
-            pu = span_unit_dot<T, AQ>(lds, span_lead(wup, start), unit, A);
-        }
+    if constexpr (ACT == ACT_F32) {
+        // fp32 activations: the wave quantizes its staged row to q8_1 blocks in LDS
+        quantize_row_lds((const float *) arow, lds + a.lds_q8, a.ncols);
+        arow = lds + a.lds_q8;
     }
-    // row sums across the nu lanes of each row (cross-lane adds, no LDS)
-    const float su = row_group_sum(pu, nu);
-    const float sg = wgate ? row_group_sum(pg, nu) : 0.0f;
-    if (active && col == 0) {
-        const int row = row0 + row_local;
-        float out;
-        if (!shared) {
-            float up = su;
-            if (a.x_scale) up *= a.x_scale[e];
-            if (a.x_bias) up += a.x_bias[(int64_t) e * a.bias_stride + row];
-            out = up;
-            if (wgate) {
-                float g = sg;
-                if (a.gate_scale) g *= a.gate_scale[e];
-                if (a.gate_bias) g += a.gate_bias[(int64_t) e * a.bias_stride + row];
-                out = glu_apply(a.glu_op, g, up, a.glu_limit);
-            }
-            a.dst[(int64_t) c * a.stride_channel_dst + (int64_t) t * a.stride_col_dst + row] = out;
-        } else {
-            out = wgate ? glu_apply(a.glu_op, sg, su, a.glu_limit) : su;
-            a.sh_dst[(int64_t) t * a.sh_stride_col_dst + row] = out;
-        }
-    }
+    float su, sg;
+    step_dots<T, AQ>(a, s, lds, arow, su, sg);
+    step_store<T>(a, s, su, sg);
 }
 
 // One wave per workgroup.  Workgroup 0 is the pick recorder when anything is
@@ -438,8 +309,11 @@ static int fit_rows_per_step(int nu, uint32_t row_bytes, int nspan, uint32_t act
     return r;
 }
 
+int launch_ffn(GemvArgs a, int tw, int ts, int act, void *stream);   // mc_ffn.hip
+
 // Fills the tiling and LDS fields of `a` and launches.  Returns a hipError_t value.
 int launch_gemv(GemvArgs a, int tw, int ts, int act, void *stream) {
+    if (a.mode != FFN_NONE) return launch_ffn(a, tw, ts, act, stream);
     const TypeGeom g = type_geom(tw);
     const int nu = a.ncols / g.unit_elems;
     const uint32_t rb = (uint32_t) nu * (uint32_t) g.unit_bytes;

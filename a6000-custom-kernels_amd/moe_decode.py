@@ -1,5 +1,13 @@
 """Synthetic multi-layer MoE decode step on the gfx950 GEMV (batch-1 decode).
 
+Two launch plans compute the same bytes (tested bit-identical):
+  fused=True (default): two launches per layer --
+    ggml_hip_moe_ffn_gate_up_norm   RMSNorm(x) * norm weight -> q8_1 inside the
+                                    gate/up GEMV (+ shared expert, SwiGLU) -> h
+    ggml_hip_moe_ffn_down_combine   down GEMV over the picks + shared expert from
+                                    the fp32 GLU rows, x' = x + shared + sum_j w_j o_j
+  fused=False: the op-by-op plan below (three launches per layer + one per token).
+
 Per layer, for one token (the op sequence of a ggml MoE FFN block):
   1. gate/up MUL_MAT_ID over the routed experts, fused SwiGLU, with the shared
      expert's gate/up in the same launch             -> h[0..n_used)   and h[n_used]
@@ -60,8 +68,9 @@ class Layer:
 
 class MoeDecodeModel:
     def __init__(self, torch, n_layers=48, n_experts=512, hidden=4096, ffn=768, n_used=8, wtype=Q2_K,
-                 sh_type=Q4_K, seed=0, device="cuda", residual=True):
+                 sh_type=Q4_K, seed=0, device="cuda", residual=True, fused=True):
         self.torch = torch
+        self.fused = fused
         self.L, self.E, self.H, self.F, self.U = n_layers, n_experts, hidden, ffn, n_used
         self.wtype, self.sh_type = wtype, sh_type
         self.residual = residual
@@ -100,25 +109,28 @@ class MoeDecodeModel:
                                   shared_src1=self.h[n_used:], shared_stride_col_y=ffn)
         self.graph = None
 
-    # bytes one token reads by definition (unique expert matrices + shared + activations + outputs)
-    def bytes_per_token(self):
-        H, F, U = self.H, self.F, self.U
-        eb_gu = row_bytes(self.wtype, H) * F
-        eb_dn = row_bytes(self.wtype, F) * H
-        sh = row_bytes(self.sh_type, H) * F * 2 + row_bytes(self.sh_type, F) * H
-        act = H // 32 * 36 + (U + 1) * F * 4          # q8_1 input row, fp32 GLU rows
-        out = (U + 1) * F * 4 + (U + 1) * H * 4
-        norm = H * 4
-        return self.L * (U * (2 * eb_gu + eb_dn) + sh + act + out + norm)
-
+    # Algorithmic bytes: unique expert matrices + shared expert + the activations
+    # and outputs each launch of the plan reads or writes once.
     def gate_up_bytes(self):
         H, F, U = self.H, self.F, self.U
-        return (U * 2 * row_bytes(self.wtype, H) * F + 2 * row_bytes(self.sh_type, H) * F
-                + H // 32 * 36 + (U + 1) * F * 4)
+        w = U * 2 * row_bytes(self.wtype, H) * F + 2 * row_bytes(self.sh_type, H) * F
+        if self.fused:                                 # x row + norm weight in, fp32 GLU rows out
+            return w + 2 * H * 4 + (U + 1) * F * 4
+        return w + H // 32 * 36 + (U + 1) * F * 4      # q8_1 row in, GLU rows out
 
     def down_bytes(self):
         H, F, U = self.H, self.F, self.U
-        return U * row_bytes(self.wtype, F) * H + row_bytes(self.sh_type, F) * H + (U + 1) * F * 4 + (U + 1) * H * 4
+        w = U * row_bytes(self.wtype, F) * H + row_bytes(self.sh_type, F) * H
+        if self.fused:                                 # GLU rows, residual, router weights in; x out
+            return w + (U + 1) * F * 4 + 2 * H * 4 + U * 4
+        return w + (U + 1) * F * 4 + (U + 1) * H * 4   # GLU rows in, expert outputs out
+
+    def combine_bytes(self):
+        H, U = self.H, self.U
+        return 0 if self.fused else (U + 1) * H * 4 + 2 * H * 4 + H * 4 + H // 32 * 36 + U * 4
+
+    def bytes_per_token(self):
+        return self.L * (self.gate_up_bytes() + self.down_bytes() + self.combine_bytes())
 
     def _stream(self):
         return C.c_void_p(self.torch.cuda.current_stream().cuda_stream)
@@ -152,9 +164,38 @@ class MoeDecodeModel:
                                               self.y.data_ptr(), H // 32, H, 1, 1, nxt.data_ptr(), self.eps, s),
               "combine")
 
+    def launch_gate_up_norm(self, l, src, s=None):
+        """Fused plan, launch 1 of layer l: gate/up GEMV on q8_1(RMSNorm(src) * norm[l])."""
+        ly = self.layers[l]
+        s = s or self._stream()
+        H, F, U = self.H, self.F, self.U
+        check(lib().ggml_hip_moe_ffn_gate_up_norm(0, C.byref(ly.t_up), None, C.byref(ly.f_gu), src.data_ptr(),
+                                                  self.norm[l].data_ptr(), self.eps, self.ids[l].data_ptr(),
+                                                  self.h.data_ptr(), H, F, self.E, 1, U, H, U * F, F, U, None, 0, s),
+              "gate_up_norm")
+
+    def launch_down_combine(self, l, src, dst, s=None):
+        """Fused plan, launch 2 of layer l: dst = src + shared + sum_j w_j * down_j(h_j)."""
+        ly = self.layers[l]
+        s = s or self._stream()
+        H, F, U = self.H, self.F, self.U
+        check(lib().ggml_hip_moe_ffn_down_combine(0, ACT_F32, C.byref(ly.t_down), C.byref(ly.f_dn),
+                                                  self.h.data_ptr(), self.ids[l].data_ptr(), self.w[l].data_ptr(),
+                                                  src.data_ptr() if self.residual else None, dst.data_ptr(),
+                                                  F, H, self.E, 1, U, (U + 1) * F, F, H, U, s),
+              "down_combine")
+
     def launch_token(self):
         """One token through every layer; the token's input and output are in self.x."""
         s = self._stream()
+        if self.fused:
+            for l in range(self.L):
+                src, dst = (self.x, self.x_next) if l % 2 == 0 else (self.x_next, self.x)
+                self.launch_gate_up_norm(l, src, s)
+                self.launch_down_combine(l, src, dst, s)
+            if self.L % 2 == 1:
+                self.x.copy_(self.x_next)
+            return
         # ffn_norm of the first MoE block and q8_1 of its output
         check(lib().ggml_hip_moe_combine_q8_1(None, 0, None, 0, None, 0, self.x.data_ptr(), None, self.y.data_ptr(),
                                               self.H // 32, self.H, 1, 1, self.norm[0].data_ptr(), self.eps, s),

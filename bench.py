@@ -6,12 +6,15 @@ shaped like the reference's (512 experts, hidden 4096, expert FFN 768, top-8
 routing with softmax router weights, Q2_K routed experts, one always-on Q4_K
 shared expert, fused SwiGLU), batch 1, every layer with its own weights
 (~76 GB resident in HBM, so the 256 MB MALL cannot serve repeat reads).  One
-token = 4 launches per layer through the C ABI, captured once as a hipGraph.
+token = 2 launches per layer through the C ABI (--plan fused: gate/up GEMV with
+the RMSNorm + q8_1 of its input in the same launch, then the down GEMV with the
+weighted combine), or 3 per layer (--plan ops: gate/up, down, combine),
+captured once as a hipGraph.
 
 value = achieved HBM GB/s of the whole step = algorithmic bytes per token
 (unique expert matrices read + activations + outputs) x tokens/s.  The
-roofline object prices the dominant kernel (the fused gate/up GEMV) with HIP
-events on its own stream.  cpu_baseline times the CPU oracle's ggml-CPU
+roofline object prices the dominant kernel (the gate/up GEMV) with HIP events
+on its own stream.  cpu_baseline times the CPU oracle's ggml-CPU
 MUL_MAT_ID restatement on this host's cores over a bounded sample of the same
 layer shape (its weights copied from the GPU).
 
@@ -72,6 +75,19 @@ def time_kernel(torch, model, launch, n_rounds):
     return e0.elapsed_time(e1) / n, n
 
 
+def gate_up_launcher(model):
+    """launch(l) of the plan's gate/up kernel (the fused plan normalizes model.x)."""
+    if model.fused:
+        return lambda l: model.launch_gate_up_norm(l, model.x)
+    return model.launch_gate_up
+
+
+def down_launcher(model):
+    if model.fused:
+        return lambda l: model.launch_down_combine(l, model.x, model.x_next)
+    return model.launch_down
+
+
 def traffic_probe(torch, model, md):
     """Kernels whose per-dispatch FETCH_SIZE / WRITE_SIZE a counter run reads: three copies of
     1 GiB (known traffic: 1 GiB read, 1 GiB written) and two gate/up GEMV launches per layer."""
@@ -85,16 +101,24 @@ def traffic_probe(torch, model, md):
     model.set_routing(torch.from_numpy(ids_np[0]).cuda(), torch.from_numpy(w_np[0]).cuda())
     model.launch_token()                     # builds every device table
     torch.cuda.synchronize()
+    launch = gate_up_launcher(model)
     for _ in range(2):
         for l in range(model.L):
-            model.launch_gate_up(l)
+            launch(l)
     torch.cuda.synchronize()
     log(f"traffic probe done: copy {4 * n} bytes x3, gate/up GEMV x{2 * model.L}")
 
 
-def load_traffic():
-    """Per-launch HBM traffic of the gate/up GEMV from the committed counter summary, or None."""
-    p = ROOT / "profiles" / "gemv_gate_up_q2K_traffic.json"
+TRAFFIC_FILES = {True: "ffn_gate_up_norm_q2K_traffic.json", False: "gemv_gate_up_q2K_traffic.json"}
+KERNEL_NAMES = {True: ("mc_ffn_gate_up_kernel<q2_K, q4_K shared> (RMSNorm + q8_1 of x, gate/up + SwiGLU)",
+                       "mc_ffn_down_combine_kernel<q2_K, q4_K shared, f32>"),
+                False: ("mc_gemv_kernel<q2_K, q4_K shared, q8_1> (fused gate/up + SwiGLU)",
+                        "mc_gemv_kernel<q2_K, q4_K shared, f32> (down)")}
+
+
+def load_traffic(fused):
+    """Per-launch HBM traffic of the plan's gate/up kernel from the committed counter summary, or None."""
+    p = ROOT / "profiles" / TRAFFIC_FILES[fused]
     if not p.exists():
         return None
     try:
@@ -150,6 +174,8 @@ def main():
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-rounds", type=int, default=10)
+    ap.add_argument("--plan", choices=("fused", "ops"), default="fused",
+                    help="fused: 2 launches per layer (default); ops: gate/up, down, combine launches")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: a 1 GiB copy (the counter calibration) and the gate/up "
                          "GEMV of every layer, then exit")
@@ -167,7 +193,8 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
 
     t0 = time.perf_counter()
-    model = md.MoeDecodeModel(torch, n_layers=args.layers)
+    fused = args.plan == "fused"
+    model = md.MoeDecodeModel(torch, n_layers=args.layers, fused=fused)
     torch.cuda.synchronize()
     log(f"weights ready: {args.layers} layers in {time.perf_counter() - t0:.1f}s, "
         f"{torch.cuda.memory_allocated() / 2**30:.1f} GiB allocated")
@@ -209,14 +236,14 @@ def main():
     gbs = bpt * tok_s / 1e9
     log(f"decode: {ms_per_tok * 1000:.1f} us/token, {tok_s:.1f} tok/s, {gbs:.1f} GB/s (wall {wall:.2f}s)")
 
-    # dominant kernel: fused gate/up GEMV (+ shared gate/up), per-launch events on its stream
-    gu_ms, n_launch = time_kernel(torch, model, model.launch_gate_up, args.kernel_rounds)
-    dn_ms, _ = time_kernel(torch, model, model.launch_down, args.kernel_rounds)
+    # dominant kernel: the gate/up GEMV (+ shared gate/up), per-launch events on its stream
+    gu_ms, n_launch = time_kernel(torch, model, gate_up_launcher(model), args.kernel_rounds)
+    dn_ms, _ = time_kernel(torch, model, down_launcher(model), args.kernel_rounds)
     gu_bytes, dn_bytes = model.gate_up_bytes(), model.down_bytes()
     gu_gbs = gu_bytes / (gu_ms * 1e-3) / 1e9
     dn_gbs = dn_bytes / (dn_ms * 1e-3) / 1e9
-    log(f"gate/up GEMV: {gu_ms * 1000:.2f} us/launch ({n_launch} launches), {gu_gbs:.0f} GB/s; "
-        f"down GEMV: {dn_ms * 1000:.2f} us/launch, {dn_gbs:.0f} GB/s")
+    log(f"gate/up: {gu_ms * 1000:.2f} us/launch ({n_launch} launches), {gu_gbs:.0f} GB/s; "
+        f"down: {dn_ms * 1000:.2f} us/launch, {dn_gbs:.0f} GB/s")
 
     cpu = None
     if not args.no_cpu:
@@ -239,16 +266,17 @@ def main():
         "config": {"workload": f"{model.L}-layer MoE decode step, B=1: 512 experts, hidden 4096, expert ffn 768, "
                                "top-8, Q2_K routed gate/up/down + Q4_K shared expert, fused SwiGLU, all resident",
                    "layers": model.L, "experts": model.E, "hidden": model.H, "ffn": model.F, "top_k": model.U,
-                   "routed_type": "q2_K", "shared_type": "q4_K", "batch": 1},
+                   "routed_type": "q2_K", "shared_type": "q4_K", "batch": 1,
+                   "plan": f"{args.plan}: {2 if fused else 3} launches per layer"},
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "tok_per_s": round(tok_s, 2),
         "bytes_per_step": bpt,
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": load_traffic(),
-                     "kernel": "mc_gemv_kernel<q2_K, q4_K shared, q8_1> (fused gate/up + SwiGLU)",
+                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": load_traffic(fused),
+                     "kernel": KERNEL_NAMES[fused][0],
                      "bytes_per_launch": gu_bytes, "us_per_launch": round(gu_ms * 1000, 3)},
-        "kernels": {"down_gemv": {"bytes_per_launch": dn_bytes, "us_per_launch": round(dn_ms * 1000, 3),
-                                  "GB/s": round(dn_gbs, 1)}},
+        "kernels": {"down": {"kernel": KERNEL_NAMES[fused][1], "bytes_per_launch": dn_bytes,
+                             "us_per_launch": round(dn_ms * 1000, 3), "GB/s": round(dn_gbs, 1)}},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

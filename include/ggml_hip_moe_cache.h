@@ -215,6 +215,44 @@ int ggml_hip_moe_combine_q8_1(const float *o, int64_t o_stride, const float *w, 
                               float *x_out, void *y_q8_1, int64_t y_stride, int64_t k, int64_t n_tok,
                               int32_t rms_norm, const float *norm_weight, float eps, void *stream);
 
+/* ---------------------------------------------------------------------
+ * Fused decode FFN block: two launches per MoE block instead of four.
+ * No reference counterpart: ggml runs RMS_NORM, MUL, quantize_q8_1,
+ * MUL_MAT_ID, the router-weight MUL and the ADDs as separate ops; these
+ * produce bit-identical results to ggml_hip_moe_combine_q8_1 followed by the
+ * MUL_MAT_ID GEMVs above (same steps, same arithmetic order).  K-quant
+ * experts (Q2_K..Q6_K) and K-quant (or no) shared experts.
+ * --------------------------------------------------------------------- */
+
+/* Gate/up MUL_MAT_ID (ggml_hip_moe_mul_mat_vec_ex arguments: src0 = up, gate via
+ * gate_host / fusion->gate, GLU, bias, scale, shared expert) whose activation is
+ * computed in the same launch from the fp32 residual rows x:
+ *   y[t] = q8_1((x[t] * (1/sqrt(mean(x[t]^2) + eps))) * norm_weight)   (norm_weight may be NULL)
+ * with the mean of squares in the canonical order of ggml_hip_moe_combine_q8_1.
+ * Every pick and the shared expert (fusion->shared_src1 must be NULL) read y[t].
+ * x: [ncols_dst][stride_col_x] floats, 16-byte aligned rows; ne00 % 256 == 0, ne00 <= 8192.
+ * y_out (optional): receives y, rows y_out_stride q8_1 blocks apart. */
+int ggml_hip_moe_ffn_gate_up_norm(
+        int use_cache, const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *gate_host,
+        const ggml_hip_moe_fusion *fusion, const float *x, const float *norm_weight, float eps,
+        const int32_t *ids_d, float *dst_d, int64_t ne00, int64_t ne01, int64_t ne02,
+        int64_t ncols_dst, int64_t nchannels_dst, int64_t stride_col_x, int64_t stride_col_dst,
+        int64_t stride_channel_dst, int64_t ids_stride, void *y_out, int64_t y_out_stride, void *stream);
+
+/* Down MUL_MAT_ID over the n_used = nchannels_dst picks of each token (pick c reads
+ * activation row src1 + t*stride_col_y + c*stride_channel_y, q8_1 blocks or floats
+ * per act_format), plus fusion->shared_up on fusion->shared_src1, combined in the
+ * same launch:
+ *   x_out[t] = residual[t] + shared[t] + sum_{c < n_used} router_w[t][c] * o_c[t]   (c ascending, fused multiply-add)
+ * residual may be NULL or equal to x_out; router_w: [ncols_dst][n_used]; x rows
+ * stride_col_x floats apart; n_used (+1 with a shared expert) <= 12.  x_bias / x_scale
+ * fusion apply to the routed picks; an out-of-range expert id contributes 0. */
+int ggml_hip_moe_ffn_down_combine(
+        int use_cache, int act_format, const ggml_hip_moe_tensor *src0, const ggml_hip_moe_fusion *fusion,
+        const void *src1, const int32_t *ids_d, const float *router_w, const float *residual, float *x_out,
+        int64_t ne00, int64_t ne01, int64_t ne02, int64_t ncols_dst, int64_t nchannels_dst,
+        int64_t stride_col_y, int64_t stride_channel_y, int64_t stride_col_x, int64_t ids_stride, void *stream);
+
 
 /* ---------------------------------------------------------------------
  * Prefill-shaped MUL_MAT_ID (many tokens).  The reference routes only batch-1

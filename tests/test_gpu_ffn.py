@@ -1,0 +1,251 @@
+"""GPU: the fused decode kernels (ggml_hip_moe_ffn_gate_up_norm and
+ggml_hip_moe_ffn_down_combine) against the op-by-op path (combine + RMSNorm +
+q8_1, then the MUL_MAT_ID GEMVs, then the weighted combine).  Both run the same
+steps in the same arithmetic order, so every output must be bit-identical; the
+op-by-op path is checked against the CPU oracle in test_gpu_decode.py and
+test_gpu_parity.py, and the fused path is also checked against the oracle here
+on its own intermediate bytes."""
+import ctypes as C
+from importlib import import_module
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+SENTINEL = -7.25
+
+
+def _note(msg):
+    print(msg, flush=True)
+
+
+def _stream(torch):
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _norm_q8_1(torch, mc, x, nw, eps):
+    """q8_1((x * rms scale) * nw) of each row through the combine kernel (no expert terms)."""
+    n_tok, K = x.shape
+    y = torch.zeros((n_tok, K // 32 * 36), dtype=torch.uint8, device="cuda")
+    mc.check(mc.lib().ggml_hip_moe_combine_q8_1(None, 0, None, 0, None, 0, x.data_ptr(), None, y.data_ptr(), K // 32,
+                                                K, n_tok, 1, nw.data_ptr() if nw is not None else None, eps,
+                                                _stream(torch)), "norm")
+    return y
+
+
+@pytest.mark.parametrize("wtype,sh_type,K,R,n_tok,with_nw,bad_id", [
+    ("Q2_K", "Q4_K", 1024, 256, 1, True, False),
+    ("Q2_K", "Q4_K", 4096, 96, 3, True, True),
+    ("Q4_K", "Q6_K", 2048, 160, 2, False, False),
+    ("Q3_K", None, 1024, 128, 1, True, False),
+    ("Q6_K", "Q5_K", 1024, 64, 2, True, True),
+    ("Q5_K", "Q2_K", 768, 200, 1, True, False),
+])
+def test_gate_up_norm_equals_norm_then_gemv(torch_gpu, mc, wtype, sh_type, K, R, n_tok, with_nw, bad_id):
+    torch = torch_gpu
+    md = import_module("a6000_custom_kernels_amd.moe_decode")
+    _note(f"gate_up_norm {wtype}/{sh_type} K={K} R={R} tok={n_tok} nw={with_nw} bad_id={bad_id}")
+    E, U, eps = 16, 4, 1e-6
+    tw = getattr(mc, wtype)
+    ts = getattr(mc, sh_type) if sh_type else None
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(K + R + n_tok)
+    up = md.random_expert_tensor(torch, tw, E, R, K, gen)
+    gate = md.random_expert_tensor(torch, tw, E, R, K, gen)
+    sh_up = md.random_expert_tensor(torch, ts, 1, R, K, gen)[0] if ts else None
+    sh_gate = md.random_expert_tensor(torch, ts, 1, R, K, gen)[0] if ts else None
+    rng = np.random.default_rng(K * 7 + n_tok)
+    x = torch.from_numpy(rng.standard_normal((n_tok, K)).astype(np.float32) * 3).cuda()
+    nw = torch.from_numpy(rng.uniform(0.5, 1.5, K).astype(np.float32)).cuda() if with_nw else None
+    ids_np = np.stack([rng.choice(E, U, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    if bad_id:
+        ids_np[-1, 1] = -1
+    ids = torch.from_numpy(ids_np).cuda()
+
+    # op by op: RMSNorm + q8_1 through the combine kernel, then the q8_1 GEMV
+    y_ref = _norm_q8_1(torch, mc, x, nw, eps)
+    dst_ref = torch.full((n_tok, U, R), SENTINEL, dtype=torch.float32, device="cuda")
+    sh_ref = torch.full((n_tok, R), SENTINEL, dtype=torch.float32, device="cuda")
+    f_ref = mc.make_fusion(gate=gate, glu_op=mc.GLU_SWIGLU, shared_up=sh_up, shared_gate=sh_gate,
+                           shared_dst=sh_ref if ts else None, shared_type=ts if ts else -1)
+    mc.mul_mat_vec(wtype=tw, weights=up, ids=ids, y=y_ref.view(n_tok, 1, -1), dst=dst_ref, K=K, R=R, n_experts=E,
+                   fusion=f_ref)
+
+    # fused
+    dst = torch.full((n_tok, U, R), SENTINEL, dtype=torch.float32, device="cuda")
+    sh = torch.full((n_tok, R), SENTINEL, dtype=torch.float32, device="cuda")
+    y_out = torch.zeros_like(y_ref)
+    f = mc.make_fusion(gate=gate, glu_op=mc.GLU_SWIGLU, shared_up=sh_up, shared_gate=sh_gate,
+                       shared_dst=sh if ts else None, shared_type=ts if ts else -1)
+    mc.ffn_gate_up_norm(wtype=tw, weights=up, ids=ids, x=x, dst=dst, K=K, R=R, n_experts=E, norm_weight=nw, eps=eps,
+                        fusion=f, y_out=y_out)
+    torch.cuda.synchronize()
+    assert torch.equal(y_out, y_ref)
+    assert torch.equal(dst, dst_ref)
+    if ts:
+        assert torch.equal(sh, sh_ref)
+    if bad_id:
+        assert bool((dst[-1, 1] == SENTINEL).all())
+    assert bool(torch.isfinite(dst[dst != SENTINEL]).all())
+
+
+@pytest.mark.parametrize("wtype,sh_type,K,R,n_tok,U,act,residual,fuse_bias,bad_id", [
+    ("Q2_K", "Q4_K", 768, 4096, 1, 8, "f32", True, False, False),
+    ("Q2_K", "Q4_K", 512, 1024, 2, 4, "q8_1", True, False, True),
+    ("Q5_K", None, 768, 1280, 3, 6, "f32", False, True, False),      # 15-row tiles, the last one partial
+    ("Q3_K", "Q6_K", 512, 512, 3, 4, "f32", True, True, True),
+    ("Q6_K", "Q4_K", 1024, 512, 1, 11, "q8_1", True, False, False),   # 12 waves per workgroup
+])
+def test_down_combine_equals_gemv_then_combine(torch_gpu, mc, wtype, sh_type, K, R, n_tok, U, act, residual,
+                                               fuse_bias, bad_id):
+    torch = torch_gpu
+    md = import_module("a6000_custom_kernels_amd.moe_decode")
+    assert R % 256 == 0                       # the op-by-op combine works on 256-value chunks
+    _note(f"down_combine {wtype}/{sh_type} K={K} R={R} tok={n_tok} U={U} act={act} res={residual} "
+          f"bias={fuse_bias} bad_id={bad_id}")
+    E = 16
+    tw = getattr(mc, wtype)
+    ts = getattr(mc, sh_type) if sh_type else None
+    act_fmt = mc.ACT_F32 if act == "f32" else mc.ACT_Q8_1
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(K + R + U)
+    down = md.random_expert_tensor(torch, tw, E, R, K, gen)
+    sh_down = md.random_expert_tensor(torch, ts, 1, R, K, gen)[0] if ts else None
+    rng = np.random.default_rng(R + n_tok)
+    h_f = torch.from_numpy(rng.standard_normal((n_tok, U, K)).astype(np.float32)).cuda()
+    hs_f = torch.from_numpy(rng.standard_normal((n_tok, K)).astype(np.float32)).cuda()
+    if act_fmt == mc.ACT_F32:
+        h, hs, sh_stride = h_f, hs_f, K
+    else:
+        h = mc.quantize_q8_1(h_f.view(n_tok * U, K)).view(n_tok, U, -1)
+        hs = mc.quantize_q8_1(hs_f)
+        sh_stride = K // 32
+    x = torch.from_numpy(rng.standard_normal((n_tok, R)).astype(np.float32)).cuda() if residual else None
+    w = torch.from_numpy(rng.dirichlet(np.ones(U), n_tok).astype(np.float32)).cuda()
+    ids_np = np.stack([rng.choice(E, U, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    if bad_id:
+        ids_np[0, U - 1] = E + 3
+    ids = torch.from_numpy(ids_np).cuda()
+    bias = torch.from_numpy(rng.standard_normal((E, R)).astype(np.float32) * 0.1).cuda() if fuse_bias else None
+    scale = torch.from_numpy(rng.uniform(0.5, 1.5, E).astype(np.float32)).cuda() if fuse_bias else None
+
+    # op by op: down GEMV (an out-of-range id leaves its rows at 0), then the combine
+    o = torch.zeros((n_tok, U, R), dtype=torch.float32, device="cuda")
+    o_sh = torch.zeros((n_tok, R), dtype=torch.float32, device="cuda")
+    f_ref = mc.make_fusion(x_bias=bias, x_scale=scale, shared_up=sh_down, shared_dst=o_sh if ts else None,
+                           shared_type=ts if ts else -1, shared_src1=hs if ts else None,
+                           shared_stride_col_y=sh_stride, bias_stride=R)
+    mc.mul_mat_vec(wtype=tw, weights=down, ids=ids, y=h, dst=o, K=K, R=R, n_experts=E, act=act_fmt, fusion=f_ref,
+                   nchannels_y=U)
+    x_ref = torch.full((n_tok, R), SENTINEL, dtype=torch.float32, device="cuda")
+    mc.combine_q8_1(o, w, shared=o_sh if ts else None, residual=x, x_out=x_ref)
+
+    x_out = torch.full((n_tok, R), SENTINEL, dtype=torch.float32, device="cuda")
+    f = mc.make_fusion(x_bias=bias, x_scale=scale, shared_up=sh_down, shared_type=ts if ts else -1,
+                       shared_src1=hs if ts else None, shared_stride_col_y=sh_stride, bias_stride=R)
+    mc.ffn_down_combine(wtype=tw, weights=down, ids=ids, h=h, router_w=w, x_out=x_out, K=K, R=R, n_experts=E,
+                        residual=x, act=act_fmt, fusion=f)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(x_ref).all())
+    assert torch.equal(x_out, x_ref)
+
+
+def test_down_combine_in_place_residual(torch_gpu, mc):
+    """residual == x_out: every row is read and written by the same lane."""
+    torch = torch_gpu
+    md = import_module("a6000_custom_kernels_amd.moe_decode")
+    E, U, K, R = 8, 4, 512, 768
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+    down = md.random_expert_tensor(torch, mc.Q2_K, E, R, K, gen)
+    rng = np.random.default_rng(5)
+    h = torch.from_numpy(rng.standard_normal((1, U, K)).astype(np.float32)).cuda()
+    x = torch.from_numpy(rng.standard_normal((1, R)).astype(np.float32)).cuda()
+    w = torch.from_numpy(rng.dirichlet(np.ones(U), 1).astype(np.float32)).cuda()
+    ids = torch.from_numpy(rng.choice(E, (1, U), replace=False).astype(np.int32)).cuda()
+    want = torch.empty_like(x)
+    mc.ffn_down_combine(wtype=mc.Q2_K, weights=down, ids=ids, h=h, router_w=w, x_out=want, K=K, R=R, n_experts=E,
+                        residual=x)
+    got = x.clone()
+    mc.ffn_down_combine(wtype=mc.Q2_K, weights=down, ids=ids, h=h, router_w=w, x_out=got, K=K, R=R, n_experts=E,
+                        residual=got)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+def test_fused_layer_against_oracle(torch_gpu, mc, O):
+    """The fused pair on its own intermediate bytes: y_out against the oracle's RMSNorm + q8_1,
+    the GLU rows against the oracle's MUL_MAT_ID on y, x_out against the oracle's down
+    projection of q8_1(h) and combine."""
+    torch = torch_gpu
+    md = import_module("a6000_custom_kernels_amd.moe_decode")
+    m = md.MoeDecodeModel(torch, n_layers=1, n_experts=16, hidden=1024, ffn=512, n_used=4, seed=9)
+    H, F, U, E = m.H, m.F, m.U, m.E
+    ids, w = md.make_routing(1, 1, E, U, seed=3)
+    rng = np.random.default_rng(8)
+    x0 = rng.standard_normal((1, H)).astype(np.float32) * 2
+    m.x.copy_(torch.from_numpy(x0))
+    m.set_routing(torch.from_numpy(ids[0]), torch.from_numpy(w[0]))
+    y_out = torch.zeros((1, H // 32 * 36), dtype=torch.uint8, device="cuda")
+    ly = m.layers[0]
+    mc.check(mc.lib().ggml_hip_moe_ffn_gate_up_norm(0, C.byref(ly.t_up), None, C.byref(ly.f_gu), m.x.data_ptr(),
+                                                    m.norm[0].data_ptr(), m.eps, m.ids[0].data_ptr(), m.h.data_ptr(),
+                                                    H, F, E, 1, U, H, U * F, F, U, y_out.data_ptr(), H // 32,
+                                                    _stream(torch)), "gate_up_norm")
+    torch.cuda.synchronize()
+    nw = m.norm[0].cpu().numpy()
+    _, want_y = O.combine_q8_1(np.zeros((1, 0, H), np.float32), np.zeros((1, 0), np.float32), residual=x0,
+                               rms_norm=True, norm_weight=nw, eps=m.eps)
+    y = y_out.cpu().numpy()
+    assert np.array_equal(y, want_y)
+    g, u, d = ly.gate.cpu().numpy(), ly.up.cpu().numpy(), ly.down.cpu().numpy()
+    sg, su, sd = ly.sh_gate.cpu().numpy(), ly.sh_up.cpu().numpy(), ly.sh_down.cpu().numpy()
+    lid = ids[0, 0].reshape(1, U)
+    h = m.h.cpu().numpy()
+    want_h, want_hs = O.mul_mat_id(wtype=m.wtype, K=H, R=F, n_as=E, src0=u, gate=g, ids=lid, act=y.reshape(1, 1, -1),
+                                   act_kind=O.ACT_Q8_1, glu_op=O.GLU_SWIGLU, sh_type=m.sh_type, sh_up=su, sh_gate=sg)
+    assert O.rel_l2(h[:U], want_h[0]) <= 1e-5
+    assert O.rel_l2(h[U], want_hs[0]) <= 1e-5
+    m.launch_down_combine(0, m.x, m.x_next)
+    torch.cuda.synchronize()
+    hq = np.stack([O.quantize_q8_1(r) for r in h])
+    want_o, want_osh = O.mul_mat_id(wtype=m.wtype, K=F, R=H, n_as=E, src0=d, ids=lid, act=hq[:U].reshape(1, U, -1),
+                                    act_kind=O.ACT_Q8_1, nchannels_y=U, sh_type=m.sh_type, sh_up=sd,
+                                    sh_act=hq[U:].reshape(1, -1))
+    want_x, _ = O.combine_q8_1(want_o, w[0, 0].reshape(1, U), shared=want_osh, residual=x0)
+    assert O.rel_l2(m.x_next.cpu().numpy(), want_x) <= 1e-5
+
+
+def test_fused_decode_equals_op_plan(torch_gpu, mc):
+    """Three tokens through the fused plan and through the op-by-op plan: identical
+    residual streams after every token, eager and under graph replay."""
+    torch = torch_gpu
+    md = import_module("a6000_custom_kernels_amd.moe_decode")
+    m = md.MoeDecodeModel(torch, n_layers=3, n_experts=16, hidden=1024, ffn=512, n_used=4, seed=5, fused=False)
+    ids, w = md.make_routing(3, m.L, m.E, m.U, seed=21)
+    ids_d, w_d = torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
+    x0 = torch.from_numpy(np.random.default_rng(6).standard_normal((1, m.H)).astype(np.float32)).cuda()
+    ref = []
+    m.x.copy_(x0)
+    for t in range(3):
+        m.set_routing(ids_d[t], w_d[t])
+        m.launch_token()
+        torch.cuda.synchronize()
+        ref.append(m.x.clone())
+    m.fused = True
+    m.x.copy_(x0)
+    for t in range(3):
+        m.set_routing(ids_d[t], w_d[t])
+        m.launch_token()
+        torch.cuda.synchronize()
+        assert torch.equal(m.x, ref[t]), f"fused token {t} differs"
+    m.x.copy_(x0)
+    m.set_routing(ids_d[0], w_d[0])
+    m.capture()
+    m.x.copy_(x0)
+    for t in range(3):
+        m.set_routing(ids_d[t], w_d[t])
+        m.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(m.x, ref[t]), f"fused replay {t} differs"

@@ -17,7 +17,9 @@ SEED_FIXTURE = ROOT / "tests" / "golden" / "moe_seed.txt"
 
 @pytest.fixture(scope="module")
 def sim(mc):
-    if not SIM.exists():
+    srcs = [ROOT / "a6000-custom-kernels_amd" / "csrc" / "mc_host.cpp", ROOT / "tests" / "native" / "sim_device.cpp",
+            ROOT / "include" / "ggml_hip_moe_cache.h"]
+    if not SIM.exists() or max(p.stat().st_mtime for p in srcs) > SIM.stat().st_mtime:
         import importlib.util
         spec = importlib.util.spec_from_file_location("mc_build", ROOT / "a6000-custom-kernels_amd" / "build.py")
         b = importlib.util.module_from_spec(spec)
