@@ -93,7 +93,7 @@ SIGNATURES = [
      [_VP, _I64, _VP, _I32, _VP, _I64, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP, C.c_float, _VP]),
     ("ggml_hip_moe_ffn_gate_up_norm", C.c_int,
      [C.c_int, C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Fusion), _VP, _VP, C.c_float, _VP, _VP]
-     + [_I64] * 3 + [_I64] * 2 + [_I64] * 4 + [_VP, _I64, _VP]),
+     + [_I64] * 3 + [_I64] * 2 + [_I64] * 4 + [_VP, _I64, _VP, _I64, _I64, _VP, _I64, _VP]),
     ("ggml_hip_moe_ffn_down_combine", C.c_int,
      [C.c_int, C.c_int, C.POINTER(Tensor), C.POINTER(Fusion), _VP, _VP, _VP, _VP, _VP]
      + [_I64] * 3 + [_I64] * 2 + [_I64] * 4 + [_VP]),
@@ -263,11 +263,12 @@ def mul_mat_vec(*, wtype, weights, ids, y, dst, K, R, n_experts, use_cache=False
 
 
 def ffn_gate_up_norm(*, wtype, weights, ids, x, dst, K, R, n_experts, norm_weight=None, eps=1e-6,
-                     fusion: Fusion | None = None, y_out=None, use_cache=False, gate_host=None, name="", stream=None,
-                     weights_ptr=None, gate_ptr=None):
+                     fusion: Fusion | None = None, y_out=None, dst_q8_1=None, shared_dst_q8_1=None, use_cache=False,
+                     gate_host=None, name="", stream=None, weights_ptr=None, gate_ptr=None):
     """Gate/up GEMV whose q8_1 activation is RMSNorm(x) * norm_weight, computed in the same launch
     (ggml_hip_moe_ffn_gate_up_norm).  x: fp32 [n_tok, K] (device, 16-byte aligned rows);
-    ids: int32 [n_tok, n_used]; dst: float32 [n_tok, n_used, R]; y_out: optional uint8 [n_tok, K/32*36]."""
+    ids: int32 [n_tok, n_used]; dst: float32 [n_tok, n_used, R]; y_out: optional uint8 [n_tok, K/32*36];
+    dst_q8_1 / shared_dst_q8_1: optional uint8 [n_tok, n_used, R/32*36] / [n_tok, R/32*36] q8_1 copies."""
     n_tok, n_used = ids.shape
     _require_gpu(ids, x, dst, norm_weight, y_out)
     keep = []
@@ -278,7 +279,10 @@ def ffn_gate_up_norm(*, wtype, weights, ids, x, dst, K, R, n_experts, norm_weigh
         1 if use_cache else 0, C.byref(src0), C.byref(g) if g is not None else None,
         C.byref(fusion) if fusion is not None else None, x.data_ptr(), _ptr(norm_weight), eps, ids.data_ptr(),
         dst.data_ptr(), K, R, n_experts, n_tok, n_used, x.stride(0), n_used * R, R, ids.stride(0),
-        _ptr(y_out), y_out.stride(0) // 36 if y_out is not None else 0, _stream(stream))
+        _ptr(y_out), y_out.stride(0) // 36 if y_out is not None else 0,
+        _ptr(dst_q8_1), dst_q8_1.stride(0) // 36 if dst_q8_1 is not None else 0,
+        dst_q8_1.stride(1) // 36 if dst_q8_1 is not None else 0,
+        _ptr(shared_dst_q8_1), shared_dst_q8_1.stride(0) // 36 if shared_dst_q8_1 is not None else 0, _stream(stream))
     check(rc, "ffn_gate_up_norm")
     return dst
 

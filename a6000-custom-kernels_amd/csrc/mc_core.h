@@ -474,10 +474,14 @@ __device__ __forceinline__ int dma_span(const uint8_t *base, u32 base_bytes, u32
     const int rounds = (int) ((lead + nbytes + 1023u) >> 10);
     constexpr int MAXR = span_lds_bytes(T) / 1024;
     const u32 lane_off = a0 + 16u * (threadIdx.x % WAVE);
+    // lanes of the last round past the span do not write LDS: the destination needs
+    // only round_up_16(lead + nbytes) bytes
+    const bool last_lane_on = 16u * (threadIdx.x % WAVE) < lead + nbytes - 1024u * (u32) (rounds - 1);
 #pragma unroll
     for (int i = 0; i < MAXR; ++i) {
         if (i < rounds) {
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * i), 16, lane_off + 1024u * i, 0, 0, 0);
+            if (i < rounds - 1 || last_lane_on)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * i), 16, lane_off + 1024u * i, 0, 0, 0);
         }
     }
     return rounds;

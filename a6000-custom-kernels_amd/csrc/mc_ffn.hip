@@ -19,10 +19,12 @@
 //     q8_1 GEMV.
 //
 //   mc_ffn_down_combine_kernel (FFN_DOWN_COMBINE)
-//     one workgroup per (token, block of rows): wave c computes the rows of pick
-//     c's down projection (wave n_used: the shared expert), the results meet in
-//     LDS, and wave 0 writes x_out = residual + shared + sum_c w_c * o_c
-//     (fmaf, c ascending) -- the combine kernel's arithmetic, without o in HBM.
+//     one workgroup per (token, block of rows): one wave per pick computes the
+//     rows of its down projection (wave 0: the shared expert, whose span is the
+//     largest), the results meet in LDS, and wave 0 writes
+//     x_out = residual + shared + sum_c w_c * o_c (fmaf, c ascending) -- the
+//     combine kernel's arithmetic, without o in HBM.  The activation rows are fp32
+//     (quantized to q8_1 by each wave) or the q8_1 rows the gate/up kernel wrote.
 //
 // A plain __syncthreads() would wait for every LDS-writing DMA of the wave
 // (its release fence drains them); lds_barrier() waits for LDS operations only,
@@ -111,11 +113,45 @@ __device__ __forceinline__ void gu_prologue(const GemvArgs &a, int t, int p, flo
     if (lane == 0) __hip_atomic_fetch_add(sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// q8_1 copy of the GLU outputs: the workgroup's steps cover exactly one 32-row block
+// of one matrix (the host arranges the tiling).  Each step wave puts its rows into the
+// LDS block (zeros for a skipped step) and counts itself; the wave that completes the
+// count quantizes the block with the q8_1 quantizer's arithmetic (32 lanes: amax and
+// sum by xor butterflies, d = amax / 127, roundf(x / d)) and writes its 36 bytes.
+__device__ __forceinline__ void gu_block_q8_1(const GemvArgs &a, int t, int local0, int sw, int rps, bool ran, int rl,
+                                              float v, float *h32, u32 *cnt) {
+    const int lane = threadIdx.x % WAVE;
+    if (ran) {
+        if (rl >= 0) h32[sw * rps + rl] = v;
+    } else if (lane < rps) {
+        h32[sw * rps + lane] = 0.0f;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");      // the rows are in LDS before the count
+    u32 old = 0u;
+    if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    old = (u32) __builtin_amdgcn_readfirstlane((int) old);
+    if (old != (u32) a.nwaves - 1) return;
+    uint8_t *blk;
+    if (local0 < a.sh_tiles_per_tok) {
+        blk = a.hq_sh + (int64_t) t * a.hq_sh_stride + (local0 * a.sh_rps / 32) * 36;
+    } else {
+        const int tile = local0 - a.sh_tiles_per_tok;
+        const int c = tile / a.tiles_per_pick;
+        blk = a.hq + (int64_t) t * a.hq_stride_col + (int64_t) c * a.hq_stride_pick +
+              ((tile % a.tiles_per_pick) * a.rps / 32) * 36;
+    }
+    const float x = lane < 32 ? h32[lane] : 0.0f;
+    float d, sum;
+    const int8_t q = q8_1_lane(x, d, sum);
+    if (lane < 32) blk[4 + lane] = (uint8_t) q;
+    if (lane == 0) *(u32 *) blk = (u32) f2h_bits(d) | ((u32) f2h_bits(sum) << 16);
+}
+
 // Workgroup: FFN_GU_PRO_WAVES prologue waves, then nwaves step waves (one GEMV step
 // each).  The step waves issue their weight spans first and only wait for the
 // normalized row once their gate span has landed; no workgroup barrier follows the
 // start, so no wave waits for another wave's weight stream.
-// Dynamic LDS: [nwaves x (up span | gate span)] [q8_1 row] [2 counters | chunk sums]
+// Dynamic LDS: [nwaves x (up span | gate span)] [q8_1 row] [4 counters | 32 chunk sums | 32-row block]
 template <int TW, int TS>
 __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void mc_ffn_gate_up_kernel(const GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -135,6 +171,7 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
         sync[0] = 0u;
         sync[1] = 0u;
         sync[2] = 0u;
+        sync[3] = 0u;
     }
     lds_barrier();                                            // counters set; nothing is in flight yet
     if (wave < NP) {
@@ -144,36 +181,43 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
         return;
     }
     const int sw = wave - NP;
-    const int local = (b % a.wg_per_tok) * a.nwaves + sw;      // this wave's step within token t
+    const int local0 = (b % a.wg_per_tok) * a.nwaves;         // the workgroup's first step within token t
+    const int local = local0 + sw;                              // this wave's step
     uint8_t *span = lds + (u32) sw * a.lds_wave;
-    const bool has_step = local < a.tiles_per_tok;
     const bool sh = local < a.sh_tiles_per_tok;
-    if (!has_step) return;
-    if constexpr (TS == 0) {
-        if (sh) return;                                       // no shared tiles without a shared type
+    bool run = local < a.tiles_per_tok && (TS != 0 || !sh);
+    StepCtx s;
+    if (run) {
+        s = sh ? step_locate(a, true, t * a.sh_tiles_per_tok + local)
+               : step_locate(a, false, t * a.n_used * a.tiles_per_pick + (local - a.sh_tiles_per_tok));
+        step_resolve(a, s);
+        run = s.valid;
     }
-    StepCtx s = sh ? step_locate(a, true, t * a.sh_tiles_per_tok + local)
-                   : step_locate(a, false, t * a.n_used * a.tiles_per_pick + (local - a.sh_tiles_per_tok));
-    step_resolve(a, s);
-    if (!s.valid) return;
-    wait_lds_count(sync + 2, (u32) NP);                       // the prologue's loads go out first
-    if (sh) {
-        if constexpr (TS != 0) step_dma<TS>(a, s, span);
-    } else {
-        step_dma<TW>(a, s, span);
-    }
-    wait_loads_at_most(s.wgate ? s.n_up : 0);                 // gate span landed (up may still land)
-    if (!wait_lds_count(sync + 1, (u32) NP)) return;          // the normalized row is complete
-    float su, sg;
-    if (sh) {
-        if constexpr (TS != 0) {
-            step_dots<TS, ACT_Q8_1>(a, s, span, ys, su, sg);
-            step_store<TS>(a, s, su, sg);
+    if (run) {
+        wait_lds_count(sync + 2, (u32) NP);                   // the prologue's loads go out first
+        if (sh) {
+            if constexpr (TS != 0) step_dma<TS>(a, s, span);
+        } else {
+            step_dma<TW>(a, s, span);
         }
-    } else {
-        step_dots<TW, ACT_Q8_1>(a, s, span, ys, su, sg);
-        step_store<TW>(a, s, su, sg);
+        wait_loads_at_most(s.wgate ? s.n_up : 0);             // gate span landed (up may still land)
+        run = wait_lds_count(sync + 1, (u32) NP);             // the normalized row is complete
     }
+    float v = 0.0f;
+    int rl = -1;
+    if (run) {
+        float su, sg;
+        if (sh) {
+            if constexpr (TS != 0) {
+                step_dots<TS, ACT_Q8_1>(a, s, span, ys, su, sg);
+                rl = step_store<TS>(a, s, su, sg, v);
+            }
+        } else {
+            step_dots<TW, ACT_Q8_1>(a, s, span, ys, su, sg);
+            rl = step_store<TW>(a, s, su, sg, v);
+        }
+    }
+    if (a.hq) gu_block_q8_1(a, t, local0, sw, sh ? a.sh_rps : a.rps, run, rl, v, red + 32, sync + 3);
 }
 
 // ---------------------------------------------------------------------------
@@ -192,13 +236,15 @@ __global__ __launch_bounds__(FFN_DN_MAX_WAVES *WAVE) void mc_ffn_down_combine_ke
     const int b = (int) blockIdx.x - a.rec;
     const int t = b / a.wg_per_tok;
     const int rt = b % a.wg_per_tok;                    // row tile
-    const bool sh = wave == a.n_used;                   // the shared expert's wave
+    // wave 0 is the shared expert's (its larger span goes out first), then pick c = wave - off
+    const int off = a.nwaves > a.n_used ? 1 : 0;
+    const bool sh = off && wave == 0;
     uint8_t *span = lds + (u32) wave * a.lds_wave;
     float *part = (float *) (lds + a.lds_part);         // [nwaves][rps]
     const int rps = a.rps;
 
     StepCtx s = sh ? step_locate(a, true, t * a.sh_tiles_per_tok + rt)
-                   : step_locate(a, false, (t * a.n_used + wave) * a.tiles_per_pick + rt);
+                   : step_locate(a, false, (t * a.n_used + wave - off) * a.tiles_per_pick + rt);
     // activation row of the wave's pick (or of the shared expert), first
     const uint8_t *ybase;
     u32 yrow, ybytes;
@@ -253,9 +299,9 @@ __global__ __launch_bounds__(FFN_DN_MAX_WAVES *WAVE) void mc_ffn_down_combine_ke
     if (wave == 0 && lane < s.nrows_here) {
         const int row = s.row0 + lane;
         float x = a.residual ? a.residual[(int64_t) t * a.x_stride + row] : 0.0f;
-        if (a.nwaves > a.n_used) x += part[a.n_used * rps + lane];
+        if (off) x += part[lane];
         const float *w = a.router_w + (int64_t) t * a.n_used;
-        for (int c = 0; c < a.n_used; ++c) x = fmaf(w[c], part[c * rps + lane], x);
+        for (int c = 0; c < a.n_used; ++c) x = fmaf(w[c], part[(c + off) * rps + lane], x);
         a.x_out[(int64_t) t * a.x_stride + row] = x;
     }
 }
@@ -317,20 +363,40 @@ static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act) {
     a.rec = (a.stats || a.stamps || a.stamps_gate) ? 1 : 0;
     if (a.mode == FFN_GATE_UP_NORM) {
         if (a.ncols % RMS_CHUNK || a.ncols > 8192) return hipErrorInvalidValue;
-        const uint32_t common = round16((uint32_t) (a.ncols / 32 * 36)) + 16u + 4u * (uint32_t) (a.ncols / RMS_CHUNK);
-        int rps = WAVE / nu, sh_rps = ts ? WAVE / nus : 0;
+        const uint32_t common = round16((uint32_t) (a.ncols / 32 * 36)) + 16u + 4u * 32u + 4u * 32u;
+        int rps, sh_rps;
+        if (a.hq) {
+            // workgroups of exactly one q8_1 block of rows: steps of a power-of-two row count
+            int r = 1;
+            while (2 * r <= WAVE / nu && 2 * r <= 32) r *= 2;
+            if (ts) {
+                int rs = 1;
+                while (2 * rs <= WAVE / nus && 2 * rs <= 32) rs *= 2;
+                if (rs < r) r = rs;
+            }
+            if (32 / r > FFN_GU_MAX_WAVES || a.nrows % 32) return hipErrorInvalidValue;
+            rps = sh_rps = r;
+            a.nwaves = 32 / r;
+        } else {
+            rps = WAVE / nu;
+            sh_rps = ts ? WAVE / nus : 0;
+        }
         for (;;) {
             a.tiles_per_pick = (a.nrows + rps - 1) / rps;
             a.sh_tiles_per_tok = ts ? (a.nrows + sh_rps - 1) / sh_rps : 0;
             a.tiles_per_tok = a.sh_tiles_per_tok + a.n_used * a.tiles_per_pick;
-            // as many waves per workgroup as fill about one workgroup per CU
-            const int want = (a.tiles_per_tok * a.n_tok + 255) / 256;
-            a.nwaves = want < 1 ? 1 : (want > FFN_GU_MAX_WAVES ? FFN_GU_MAX_WAVES : want);
-            const uint32_t sr = span_bytes((uint32_t) rps, rb);
-            const uint32_t ss = ts ? span_bytes((uint32_t) sh_rps, rbs) : 0u;
+            if (!a.hq) {
+                // as many step waves per workgroup as fill about one workgroup per CU
+                const int want = (a.tiles_per_tok * a.n_tok + 255) / 256;
+                a.nwaves = want < 1 ? 1 : (want > FFN_GU_MAX_WAVES ? FFN_GU_MAX_WAVES : want);
+            }
+            // spans sized to the 16-byte chunk the DMA writes last (+ lead-in and over-read)
+            const uint32_t sr = round16((uint32_t) rps * rb + 20u);
+            const uint32_t ss = ts ? round16((uint32_t) sh_rps * rbs + 20u) : 0u;
             a.lds_span = sr > ss ? sr : ss;
             a.lds_wave = (uint32_t) nspan * a.lds_span;
             if ((uint32_t) a.nwaves * a.lds_wave + common <= FFN_LDS_MAX) break;
+            if (a.hq) return hipErrorInvalidValue;
             if (ts && ss >= sr && sh_rps > 1) --sh_rps;
             else if (rps > 1) --rps;
             else return hipErrorInvalidValue;
@@ -340,7 +406,7 @@ static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act) {
         a.wg_per_tok = (a.tiles_per_tok + a.nwaves - 1) / a.nwaves;
         a.lds_y = (uint32_t) a.nwaves * a.lds_wave;
         a.lds_part = a.lds_y + round16((uint32_t) (a.ncols / 32 * 36));
-        a.lds_total = a.lds_part + 16u + 4u * (uint32_t) (a.ncols / RMS_CHUNK);
+        a.lds_total = a.lds_part + 16u + 4u * 32u + 4u * 32u;
         a.n_tiles = a.tiles_per_tok * a.n_tok;
         return hipSuccess;
     }

@@ -489,6 +489,10 @@ struct FfnExtra {
     float eps = 0.0f;
     uint8_t *y_out = nullptr;
     int64_t y_out_stride = 0;
+    uint8_t *hq = nullptr;
+    int64_t hq_stride_col = 0, hq_stride_pick = 0;
+    uint8_t *hq_sh = nullptr;
+    int64_t hq_sh_stride = 0;
     const float *router_w = nullptr;
     const float *residual = nullptr;
     float *x_out = nullptr;
@@ -646,6 +650,11 @@ int gemv_common(int use_cache, int act, const ggml_hip_moe_tensor *src0, const g
         a.eps = fx->eps;
         a.y_out = fx->y_out;
         a.y_out_stride = fx->y_out_stride;
+        a.hq = fx->hq;
+        a.hq_stride_col = fx->hq_stride_col;
+        a.hq_stride_pick = fx->hq_stride_pick;
+        a.hq_sh = fx->hq_sh;
+        a.hq_sh_stride = fx->hq_sh_stride;
         a.router_w = fx->router_w;
         a.residual = fx->residual;
         a.x_out = fx->x_out;
@@ -737,8 +746,17 @@ int ggml_hip_moe_ffn_gate_up_norm(int use_cache, const ggml_hip_moe_tensor *src0
                                   const int32_t *ids_d, float *dst_d, int64_t ne00, int64_t ne01, int64_t ne02,
                                   int64_t ncols_dst, int64_t nchannels_dst, int64_t stride_col_x, int64_t stride_col_dst,
                                   int64_t stride_channel_dst, int64_t ids_stride, void *y_out, int64_t y_out_stride,
-                                  void *stream) {
+                                  void *dst_q8_1, int64_t q8_stride_col, int64_t q8_stride_channel,
+                                  void *shared_dst_q8_1, int64_t shared_q8_stride_col, void *stream) {
     if (!x) return fail(E_INVALID, "moe-ffn: null x");
+    if (dst_q8_1) {
+        if (ne01 % 32) return fail(E_UNSUPPORTED, "moe-ffn: q8_1 outputs need ne01 %% 32 == 0");
+        if (ne00 / 256 > 16) return fail(E_UNSUPPORTED, "moe-ffn: q8_1 outputs need at most 16 units per row");
+        if ((((uintptr_t) dst_q8_1) | ((uintptr_t) shared_dst_q8_1)) & 3u)
+            return fail(E_INVALID, "moe-ffn: q8_1 outputs must be 4-byte aligned");
+        if (fusion && fusion->shared_up && !shared_dst_q8_1)
+            return fail(E_INVALID, "moe-ffn: q8_1 outputs with a shared expert need shared_dst_q8_1");
+    }
     if (use_cache && !wants_impl(src0)) return fail(E_STATE, "moe-cache: src0 does not qualify for the cache path (wants() == 0)");
     if (!use_cache && gate_host) return fail(E_INVALID, "moe-gemv: gate_host is for the cache path; pass fusion->gate");
     if (ne00 <= 0 || ne00 % 256 || ne00 > 8192) return fail(E_UNSUPPORTED, "moe-ffn: ne00=%lld must be a multiple of 256 up to 8192", (long long) ne00);
@@ -756,6 +774,11 @@ int ggml_hip_moe_ffn_gate_up_norm(int use_cache, const ggml_hip_moe_tensor *src0
     fx.eps = eps;
     fx.y_out = (uint8_t *) y_out;
     fx.y_out_stride = y_out_stride * 36;
+    fx.hq = (uint8_t *) dst_q8_1;
+    fx.hq_stride_col = q8_stride_col * 36;
+    fx.hq_stride_pick = q8_stride_channel * 36;
+    fx.hq_sh = (uint8_t *) shared_dst_q8_1;
+    fx.hq_sh_stride = shared_q8_stride_col * 36;
     // the dots read the q8_1 row built in LDS; src1 stands in for the activation argument
     return gemv_common(use_cache ? 1 : 0, ACT_Q8_1, src0, gate_host, fusion, x, ids_d, dst_d, ne00, ne01, ne02, ncols_dst,
                        1, nchannels_dst, 0, stride_col_dst, 0, stride_channel_dst, ids_stride, stream, &fx);

@@ -144,6 +144,11 @@ struct GemvArgs {
     float eps;
     uint8_t *y_out;               // optional copy of the q8_1 rows (written by each token's first workgroup)
     int64_t y_out_stride;         // bytes
+    uint8_t *hq;                  // optional q8_1 copy of the routed outputs: pick c of token t at
+    int64_t hq_stride_col;        //   hq + t * hq_stride_col + c * hq_stride_pick (bytes); needs
+    int64_t hq_stride_pick;       //   workgroups of exactly 32 rows of one matrix (one q8_1 block)
+    uint8_t *hq_sh;               // ... of the shared expert's output: hq_sh + t * hq_sh_stride
+    int64_t hq_sh_stride;
     // FFN_DOWN_COMBINE: x_out = residual + shared + sum_c router_w[c] * o_c (c ascending, fmaf)
     const float *router_w;        // [n_tok][n_used]
     const float *residual;        // [n_tok][x_stride], or null

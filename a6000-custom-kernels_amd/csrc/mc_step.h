@@ -222,19 +222,34 @@ __device__ __forceinline__ float routed_value(const GemvArgs &a, const StepCtx &
     return glu_apply(a.glu_op, g, up, a.glu_limit);
 }
 
-// Stores the step's rows to dst (routed) or sh_dst (shared).
+// The output value of the row this lane reports (the first lane of each row group);
+// returns the row's index within the step, or -1 for the other lanes.
 template <int T>
-__device__ __forceinline__ void step_store(const GemvArgs &a, const StepCtx &s, float su, float sg) {
+__device__ __forceinline__ int step_value(const GemvArgs &a, const StepCtx &s, float su, float sg, float &v) {
     const int lane = threadIdx.x % WAVE;
     const int nu = a.ncols / type_geom(T).unit_elems;
     const int row_local = lane / nu, col = lane % nu;
-    if (row_local >= s.nrows_here || col != 0) return;
+    if (row_local >= s.nrows_here || col != 0) return -1;
     const int row = s.row0 + row_local;
-    if (!s.shared) {
-        a.dst[(int64_t) s.c * a.stride_channel_dst + (int64_t) s.t * a.stride_col_dst + row] = routed_value(a, s, row, su, sg);
-    } else {
-        a.sh_dst[(int64_t) s.t * a.sh_stride_col_dst + row] = s.wgate ? glu_apply(a.glu_op, sg, su, a.glu_limit) : su;
-    }
+    v = s.shared ? (s.wgate ? glu_apply(a.glu_op, sg, su, a.glu_limit) : su) : routed_value(a, s, row, su, sg);
+    return row_local;
+}
+
+// Stores the step's rows to dst (routed) or sh_dst (shared); returns step_value's row.
+template <int T>
+__device__ __forceinline__ int step_store(const GemvArgs &a, const StepCtx &s, float su, float sg, float &v) {
+    const int rl = step_value<T>(a, s, su, sg, v);
+    if (rl < 0) return rl;
+    const int row = s.row0 + rl;
+    if (!s.shared) a.dst[(int64_t) s.c * a.stride_channel_dst + (int64_t) s.t * a.stride_col_dst + row] = v;
+    else a.sh_dst[(int64_t) s.t * a.sh_stride_col_dst + row] = v;
+    return rl;
+}
+
+template <int T>
+__device__ __forceinline__ void step_store(const GemvArgs &a, const StepCtx &s, float su, float sg) {
+    float v;
+    step_store<T>(a, s, su, sg, v);
 }
 
 }  // namespace mc

@@ -3,9 +3,10 @@
 Two launch plans compute the same bytes (tested bit-identical):
   fused=True (default): two launches per layer --
     ggml_hip_moe_ffn_gate_up_norm   RMSNorm(x) * norm weight -> q8_1 inside the
-                                    gate/up GEMV (+ shared expert, SwiGLU) -> h
+                                    gate/up GEMV (+ shared expert, SwiGLU) -> h and
+                                    its q8_1 copy hq
     ggml_hip_moe_ffn_down_combine   down GEMV over the picks + shared expert from
-                                    the fp32 GLU rows, x' = x + shared + sum_j w_j o_j
+                                    hq, x' = x + shared + sum_j w_j o_j
   fused=False: the op-by-op plan below (three launches per layer + one per token).
 
 Per layer, for one token (the op sequence of a ggml MoE FFN block):
@@ -96,6 +97,7 @@ class MoeDecodeModel:
         self.x_next = torch.zeros((1, hidden), dtype=f32, device=device)
         self.y = torch.zeros((1, hidden // 32 * 36), dtype=u8, device=device)
         self.h = torch.zeros((n_used + 1, ffn), dtype=f32, device=device)   # row n_used: shared expert
+        self.hq = torch.zeros((n_used + 1, ffn // 32 * 36), dtype=u8, device=device)   # q8_1 copy of h
         self.o = torch.zeros((n_used, hidden), dtype=f32, device=device)
         self.o_sh = torch.zeros((1, hidden), dtype=f32, device=device)
         self.ids = torch.zeros((n_layers, 1, n_used), dtype=i32, device=device)
@@ -107,6 +109,8 @@ class MoeDecodeModel:
                                   shared_dst=self.h[n_used:], shared_type=sh_type)
             ly.f_dn = make_fusion(shared_up=ly.sh_down, shared_dst=self.o_sh, shared_type=sh_type,
                                   shared_src1=self.h[n_used:], shared_stride_col_y=ffn)
+            ly.f_dnq = make_fusion(shared_up=ly.sh_down, shared_type=sh_type, shared_src1=self.hq[n_used:],
+                                   shared_stride_col_y=ffn // 32)
         self.graph = None
 
     # Algorithmic bytes: unique expert matrices + shared expert + the activations
@@ -114,15 +118,15 @@ class MoeDecodeModel:
     def gate_up_bytes(self):
         H, F, U = self.H, self.F, self.U
         w = U * 2 * row_bytes(self.wtype, H) * F + 2 * row_bytes(self.sh_type, H) * F
-        if self.fused:                                 # x row + norm weight in, fp32 GLU rows out
-            return w + 2 * H * 4 + (U + 1) * F * 4
+        if self.fused:                                 # x row + norm weight in, GLU rows (fp32 + q8_1) out
+            return w + 2 * H * 4 + (U + 1) * F * 4 + (U + 1) * F // 32 * 36
         return w + H // 32 * 36 + (U + 1) * F * 4      # q8_1 row in, GLU rows out
 
     def down_bytes(self):
         H, F, U = self.H, self.F, self.U
         w = U * row_bytes(self.wtype, F) * H + row_bytes(self.sh_type, F) * H
-        if self.fused:                                 # GLU rows, residual, router weights in; x out
-            return w + (U + 1) * F * 4 + 2 * H * 4 + U * 4
+        if self.fused:                                 # q8_1 GLU rows, residual, router weights in; x out
+            return w + (U + 1) * F // 32 * 36 + 2 * H * 4 + U * 4
         return w + (U + 1) * F * 4 + (U + 1) * H * 4   # GLU rows in, expert outputs out
 
     def combine_bytes(self):
@@ -169,9 +173,12 @@ class MoeDecodeModel:
         ly = self.layers[l]
         s = s or self._stream()
         H, F, U = self.H, self.F, self.U
+        nb = F // 32
         check(lib().ggml_hip_moe_ffn_gate_up_norm(0, C.byref(ly.t_up), None, C.byref(ly.f_gu), src.data_ptr(),
                                                   self.norm[l].data_ptr(), self.eps, self.ids[l].data_ptr(),
-                                                  self.h.data_ptr(), H, F, self.E, 1, U, H, U * F, F, U, None, 0, s),
+                                                  self.h.data_ptr(), H, F, self.E, 1, U, H, U * F, F, U, None, 0,
+                                                  self.hq.data_ptr(), (U + 1) * nb, nb,
+                                                  self.hq[U:].data_ptr(), (U + 1) * nb, s),
               "gate_up_norm")
 
     def launch_down_combine(self, l, src, dst, s=None):
@@ -179,10 +186,11 @@ class MoeDecodeModel:
         ly = self.layers[l]
         s = s or self._stream()
         H, F, U = self.H, self.F, self.U
-        check(lib().ggml_hip_moe_ffn_down_combine(0, ACT_F32, C.byref(ly.t_down), C.byref(ly.f_dn),
-                                                  self.h.data_ptr(), self.ids[l].data_ptr(), self.w[l].data_ptr(),
+        nb = F // 32
+        check(lib().ggml_hip_moe_ffn_down_combine(0, ACT_Q8_1, C.byref(ly.t_down), C.byref(ly.f_dnq),
+                                                  self.hq.data_ptr(), self.ids[l].data_ptr(), self.w[l].data_ptr(),
                                                   src.data_ptr() if self.residual else None, dst.data_ptr(),
-                                                  F, H, self.E, 1, U, (U + 1) * F, F, H, U, s),
+                                                  F, H, self.E, 1, U, (U + 1) * nb, nb, H, U, s),
               "down_combine")
 
     def launch_token(self):

@@ -231,13 +231,20 @@ int ggml_hip_moe_combine_q8_1(const float *o, int64_t o_stride, const float *w, 
  * with the mean of squares in the canonical order of ggml_hip_moe_combine_q8_1.
  * Every pick and the shared expert (fusion->shared_src1 must be NULL) read y[t].
  * x: [ncols_dst][stride_col_x] floats, 16-byte aligned rows; ne00 % 256 == 0, ne00 <= 8192.
- * y_out (optional): receives y, rows y_out_stride q8_1 blocks apart. */
+ * y_out (optional): receives y, rows y_out_stride q8_1 blocks apart.
+ * dst_q8_1 / shared_dst_q8_1 (optional, both or neither with a shared expert): the q8_1
+ * quantization of the outputs (the down projection's input, as ggml_hip_quantize_q8_1 of
+ * dst would give), pick c of token t at dst_q8_1 + (t*q8_stride_col + c*q8_stride_channel)
+ * q8_1 blocks, the shared expert's at shared_dst_q8_1 + t*shared_q8_stride_col blocks;
+ * needs ne01 % 32 == 0 and at most 16 units per row (ne00 <= 4096). */
 int ggml_hip_moe_ffn_gate_up_norm(
         int use_cache, const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *gate_host,
         const ggml_hip_moe_fusion *fusion, const float *x, const float *norm_weight, float eps,
         const int32_t *ids_d, float *dst_d, int64_t ne00, int64_t ne01, int64_t ne02,
         int64_t ncols_dst, int64_t nchannels_dst, int64_t stride_col_x, int64_t stride_col_dst,
-        int64_t stride_channel_dst, int64_t ids_stride, void *y_out, int64_t y_out_stride, void *stream);
+        int64_t stride_channel_dst, int64_t ids_stride, void *y_out, int64_t y_out_stride,
+        void *dst_q8_1, int64_t q8_stride_col, int64_t q8_stride_channel,
+        void *shared_dst_q8_1, int64_t shared_q8_stride_col, void *stream);
 
 /* Down MUL_MAT_ID over the n_used = nchannels_dst picks of each token (pick c reads
  * activation row src1 + t*stride_col_y + c*stride_channel_y, q8_1 blocks or floats

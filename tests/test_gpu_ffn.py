@@ -78,13 +78,24 @@ def test_gate_up_norm_equals_norm_then_gemv(torch_gpu, mc, wtype, sh_type, K, R,
     y_out = torch.zeros_like(y_ref)
     f = mc.make_fusion(gate=gate, glu_op=mc.GLU_SWIGLU, shared_up=sh_up, shared_gate=sh_gate,
                        shared_dst=sh if ts else None, shared_type=ts if ts else -1)
+    q8 = R % 32 == 0 and K <= 4096            # q8_1 copies of the outputs need 32-row blocks
+    dq = torch.zeros((n_tok, U, R // 32 * 36), dtype=torch.uint8, device="cuda") if q8 else None
+    shq = torch.zeros((n_tok, R // 32 * 36), dtype=torch.uint8, device="cuda") if q8 and ts else None
     mc.ffn_gate_up_norm(wtype=tw, weights=up, ids=ids, x=x, dst=dst, K=K, R=R, n_experts=E, norm_weight=nw, eps=eps,
-                        fusion=f, y_out=y_out)
+                        fusion=f, y_out=y_out, dst_q8_1=dq, shared_dst_q8_1=shq)
     torch.cuda.synchronize()
     assert torch.equal(y_out, y_ref)
     assert torch.equal(dst, dst_ref)
     if ts:
         assert torch.equal(sh, sh_ref)
+    if q8:
+        # bit-identical to the q8_1 quantizer run on the fp32 outputs (skipped picks excepted)
+        for ti in range(n_tok):
+            for c in range(U):
+                if ids_np[ti, c] >= 0:
+                    assert torch.equal(dq[ti, c], mc.quantize_q8_1(dst[ti, c].view(1, R))[0]), (ti, c)
+            if ts:
+                assert torch.equal(shq[ti], mc.quantize_q8_1(sh[ti].view(1, R))[0])
     if bad_id:
         assert bool((dst[-1, 1] == SENTINEL).all())
     assert bool(torch.isfinite(dst[dst != SENTINEL]).all())
@@ -192,7 +203,9 @@ def test_fused_layer_against_oracle(torch_gpu, mc, O):
     mc.check(mc.lib().ggml_hip_moe_ffn_gate_up_norm(0, C.byref(ly.t_up), None, C.byref(ly.f_gu), m.x.data_ptr(),
                                                     m.norm[0].data_ptr(), m.eps, m.ids[0].data_ptr(), m.h.data_ptr(),
                                                     H, F, E, 1, U, H, U * F, F, U, y_out.data_ptr(), H // 32,
-                                                    _stream(torch)), "gate_up_norm")
+                                                    m.hq.data_ptr(), (U + 1) * F // 32, F // 32,
+                                                    m.hq[U:].data_ptr(), (U + 1) * F // 32, _stream(torch)),
+             "gate_up_norm")
     torch.cuda.synchronize()
     nw = m.norm[0].cpu().numpy()
     _, want_y = O.combine_q8_1(np.zeros((1, 0, H), np.float32), np.zeros((1, 0), np.float32), residual=x0,
@@ -203,6 +216,7 @@ def test_fused_layer_against_oracle(torch_gpu, mc, O):
     sg, su, sd = ly.sh_gate.cpu().numpy(), ly.sh_up.cpu().numpy(), ly.sh_down.cpu().numpy()
     lid = ids[0, 0].reshape(1, U)
     h = m.h.cpu().numpy()
+    assert np.array_equal(m.hq.cpu().numpy(), np.stack([O.quantize_q8_1(r) for r in h]))   # q8_1 copy of h
     want_h, want_hs = O.mul_mat_id(wtype=m.wtype, K=H, R=F, n_as=E, src0=u, gate=g, ids=lid, act=y.reshape(1, 1, -1),
                                    act_kind=O.ACT_Q8_1, glu_op=O.GLU_SWIGLU, sh_type=m.sh_type, sh_up=su, sh_gate=sg)
     assert O.rel_l2(h[:U], want_h[0]) <= 1e-5
