@@ -72,7 +72,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 // aligned (q8_1 slices of 256 values are 288 bytes: 18 chunks) the slice is read
 // with 128-bit LDS reads, else with 32-bit reads.
 template <int UE, int ACT>
-__device__ __forceinline__ void load_act_lds(Act<UE> &A, const uint8_t *p) {
+__device__ __forceinline__ void load_act_lds(Act<UE> &A, const uint8_t *p, const int16_t *s16 = nullptr) {
     constexpr int NW = ACT == ACT_Q8_1 ? UE / 32 * 9 : 73;
     u32 w[NW];
     if (NW % 4 == 0 && ((uintptr_t) p & 15u) == 0) {
@@ -105,7 +105,18 @@ __device__ __forceinline__ void load_act_lds(Act<UE> &A, const uint8_t *p) {
 #pragma unroll
         for (int k = 0; k < 64; ++k) A.q[k] = w[1 + k];
     }
-    act_sums(A);
+    if (s16) {
+        // the 16-value sums precomputed next to the row (exact integer sums of the same codes)
+        const u32 *sw = (const u32 *) s16;
+#pragma unroll
+        for (int i = 0; i < UE / 32; ++i) {
+            const u32 pair = sw[i];
+            A.s16[2 * i] = (int) (int16_t) (pair & 0xFFFFu);
+            A.s16[2 * i + 1] = (int) (int16_t) (pair >> 16);
+        }
+    } else {
+        act_sums(A);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -733,7 +744,7 @@ __device__ __forceinline__ float max8(float v) {
 // WITH_SUM = false leaves the sum field 0: the K-quant dots read only d and the codes.
 template <bool WITH_SUM = true>
 __device__ __forceinline__ void quantize_chunk(const float xv[4], bool norm, float s, const v4f nwv, uint8_t *y,
-                                               int j) {
+                                               int j, int16_t *s16 = nullptr) {
     const int lane = threadIdx.x % WAVE;
     float v[4] = {xv[0], xv[1], xv[2], xv[3]};
     if (norm) {
@@ -754,16 +765,28 @@ __device__ __forceinline__ void quantize_chunk(const float xv[4], bool norm, flo
         sum = t2[0] + t2[1];
     }
     const float d = amax / 127.0f;
+    // every quotient is computed (by 1 when amax is 0, where the select gives 0 anyway), so
+    // the four divisions are straight-line code the scheduler can interleave
+    const float dq = amax == 0.0f ? 1.0f : d;
     u32 packed = 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const int code = amax == 0.0f ? 0 : (int) roundf(v[k] / d);
+        const int q = (int) roundf(v[k] / dq);
+        const int code = amax == 0.0f ? 0 : q;
         packed |= ((u32) code & 0xFFu) << (8 * k);
     }
     const int i = j * RMS_CHUNK + 4 * lane;               // first value of this lane in the row
     uint8_t *yb = y + (i / 32) * 36;
     *(u32 *) (yb + 4 + (i % 32)) = packed;
-    if ((lane & 7) == 0) *(u32 *) yb = (u32) f2h_bits(d) | (WITH_SUM ? ((u32) f2h_bits(sum) << 16) : 0u);
+    // the eight lanes of a block store the same scale word (no branch around the store)
+    *(u32 *) yb = (u32) f2h_bits(d) | (WITH_SUM ? ((u32) f2h_bits(sum) << 16) : 0u);
+    if (s16) {
+        // sums of each 16 codes of the chunk (lanes 4m .. 4m+3 hold sub-block m): quad sums by DPP
+        int cs = sdot4(packed, 0x01010101u, 0);
+        cs += __builtin_amdgcn_update_dpp(0, cs, 0xB1, 0xF, 0xF, false);
+        cs += __builtin_amdgcn_update_dpp(0, cs, 0x4E, 0xF, 0xF, false);
+        s16[16 * j + lane / 4] = (int16_t) cs;    // the four lanes of a quad store the same value
+    }
 }
 
 }  // namespace mc

@@ -66,8 +66,8 @@ __device__ __forceinline__ bool wait_lds_count(const u32 *cnt, u32 n) {
 // other prologue waves' sums, and writes q8_1((x * scale) * nw) of its chunks to the
 // LDS row (and to y_out when asked), counted in sync[1].
 template <int PC>
-__device__ __forceinline__ void gu_prologue(const GemvArgs &a, int t, int p, float *red, uint8_t *ys, u32 *sync,
-                                            bool write_y_out) {
+__device__ __forceinline__ void gu_prologue(const GemvArgs &a, int t, int p, float *red, uint8_t *ys, int16_t *s16,
+                                            u32 *sync, bool write_y_out) {
     constexpr int NP = FFN_GU_PRO_WAVES;
     const int lane = threadIdx.x % WAVE;
     const int K = a.ncols, nchunk = K / RMS_CHUNK;
@@ -99,7 +99,7 @@ __device__ __forceinline__ void gu_prologue(const GemvArgs &a, int t, int p, flo
 #pragma unroll
     for (int ci = 0; ci < PC; ++ci) {
         const float x4[4] = {xv[ci].x, xv[ci].y, xv[ci].z, xv[ci].w};
-        quantize_chunk<false>(x4, true, scale, nwv[ci], ys, min(p + NP * ci, nchunk - 1));
+        quantize_chunk<false>(x4, true, scale, nwv[ci], ys, min(p + NP * ci, nchunk - 1), s16);
     }
     if (write_y_out) {
 #pragma unroll
@@ -151,7 +151,8 @@ __device__ __forceinline__ void gu_block_q8_1(const GemvArgs &a, int t, int loca
 // each).  The step waves issue their weight spans first and only wait for the
 // normalized row once their gate span has landed; no workgroup barrier follows the
 // start, so no wave waits for another wave's weight stream.
-// Dynamic LDS: [nwaves x (up span | gate span)] [q8_1 row] [4 counters | 32 chunk sums | 32-row block]
+// Dynamic LDS: [nwaves x (up span | gate span)] [q8_1 row] [4 counters | 32 chunk sums | 32-row block |
+// 16-value sums of the row (int16)]
 template <int TW, int TS>
 __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void mc_ffn_gate_up_kernel(const GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -167,6 +168,7 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
     uint8_t *ys = lds + a.lds_y;
     u32 *sync = (u32 *) (lds + a.lds_part);
     float *red = (float *) (lds + a.lds_part + 16);
+    int16_t *s16 = (int16_t *) (lds + a.lds_part + 16 + 4 * 32 + 4 * 32);   // 16-value sums of y
     if (threadIdx.x == 0) {
         sync[0] = 0u;
         sync[1] = 0u;
@@ -176,8 +178,8 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
     lds_barrier();                                            // counters set; nothing is in flight yet
     if (wave < NP) {
         const bool y_out = a.y_out && (b % a.wg_per_tok) == 0;
-        if (a.ncols <= 4 * NP * RMS_CHUNK) gu_prologue<4>(a, t, wave, red, ys, sync, y_out);
-        else gu_prologue<8192 / RMS_CHUNK / NP>(a, t, wave, red, ys, sync, y_out);
+        if (a.ncols <= 4 * NP * RMS_CHUNK) gu_prologue<4>(a, t, wave, red, ys, s16, sync, y_out);
+        else gu_prologue<8192 / RMS_CHUNK / NP>(a, t, wave, red, ys, s16, sync, y_out);
         return;
     }
     const int sw = wave - NP;
@@ -209,11 +211,11 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
         float su, sg;
         if (sh) {
             if constexpr (TS != 0) {
-                step_dots<TS, ACT_Q8_1>(a, s, span, ys, su, sg);
+                step_dots<TS, ACT_Q8_1>(a, s, span, ys, su, sg, s16);
                 rl = step_store<TS>(a, s, su, sg, v);
             }
         } else {
-            step_dots<TW, ACT_Q8_1>(a, s, span, ys, su, sg);
+            step_dots<TW, ACT_Q8_1>(a, s, span, ys, su, sg, s16);
             rl = step_store<TW>(a, s, su, sg, v);
         }
     }
@@ -363,7 +365,8 @@ static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act) {
     a.rec = (a.stats || a.stamps || a.stamps_gate) ? 1 : 0;
     if (a.mode == FFN_GATE_UP_NORM) {
         if (a.ncols % RMS_CHUNK || a.ncols > 8192) return hipErrorInvalidValue;
-        const uint32_t common = round16((uint32_t) (a.ncols / 32 * 36)) + 16u + 4u * 32u + 4u * 32u;
+        const uint32_t common = round16((uint32_t) (a.ncols / 32 * 36)) + 16u + 4u * 32u + 4u * 32u +
+                                2u * (uint32_t) (a.ncols / 16);
         int rps, sh_rps;
         if (a.hq) {
             // workgroups of exactly one q8_1 block of rows: steps of a power-of-two row count
@@ -406,7 +409,7 @@ static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act) {
         a.wg_per_tok = (a.tiles_per_tok + a.nwaves - 1) / a.nwaves;
         a.lds_y = (uint32_t) a.nwaves * a.lds_wave;
         a.lds_part = a.lds_y + round16((uint32_t) (a.ncols / 32 * 36));
-        a.lds_total = a.lds_part + 16u + 4u * 32u + 4u * 32u;
+        a.lds_total = a.lds_part + 16u + 4u * 32u + 4u * 32u + 2u * (uint32_t) (a.ncols / 16);
         a.n_tiles = a.tiles_per_tok * a.n_tok;
         return hipSuccess;
     }

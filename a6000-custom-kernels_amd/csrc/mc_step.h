@@ -179,7 +179,7 @@ __device__ __forceinline__ void step_issue(const GemvArgs &a, StepCtx &s, uint8_
 // for here.  Returns the row sums (valid in lane row_local * nu of each row).
 template <int T, int AQ>
 __device__ __forceinline__ void step_dots(const GemvArgs &a, const StepCtx &s, const uint8_t *span,
-                                          const uint8_t *arow, float &su, float &sg) {
+                                          const uint8_t *arow, float &su, float &sg, const int16_t *s16 = nullptr) {
     constexpr TypeGeom G = type_geom(T);
     constexpr int UE = G.unit_elems;
     constexpr int AUB = AQ == ACT_Q8_1 ? UE / 32 * 36 : 292;     // activation bytes per unit
@@ -191,9 +191,11 @@ __device__ __forceinline__ void step_dots(const GemvArgs &a, const StepCtx &s, c
     const uint8_t *aslice = arow + (u32) col * AUB;
     Act<UE> A;
     float pu = 0.0f, pg = 0.0f;
+    // precomputed 16-value activation sums of the unit, when the caller has them (K-quant units)
+    const int16_t *us16 = s16 ? s16 + (u32) col * (UE / 16) : nullptr;
     if (s.wgate) {
         if (active) {
-            load_act_lds<UE, AQ>(A, aslice);
+            load_act_lds<UE, AQ>(A, aslice, us16);
             pg = span_unit_dot<T, AQ>(span + a.lds_span, span_lead(s.wgate, s.start), unit, A);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -201,7 +203,7 @@ __device__ __forceinline__ void step_dots(const GemvArgs &a, const StepCtx &s, c
     } else {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         if (active) {
-            load_act_lds<UE, AQ>(A, aslice);
+            load_act_lds<UE, AQ>(A, aslice, us16);
             pu = span_unit_dot<T, AQ>(span, span_lead(s.wup, s.start), unit, A);
         }
     }
