@@ -111,7 +111,7 @@ def traffic_probe(torch, model, md):
 
 TRAFFIC_FILES = {True: "ffn_gate_up_norm_q2K_traffic.json", False: "gemv_gate_up_q2K_traffic.json"}
 KERNEL_NAMES = {True: ("mc_ffn_gate_up_kernel<q2_K, q4_K shared> (RMSNorm + q8_1 of x, gate/up + SwiGLU)",
-                       "mc_ffn_down_combine_kernel<q2_K, q4_K shared, f32>"),
+                       "mc_ffn_down_combine_kernel<q2_K, q4_K shared, q8_1> (down + weighted combine)"),
                 False: ("mc_gemv_kernel<q2_K, q4_K shared, q8_1> (fused gate/up + SwiGLU)",
                         "mc_gemv_kernel<q2_K, q4_K shared, f32> (down)")}
 
