@@ -263,3 +263,76 @@ def test_fused_decode_equals_op_plan(torch_gpu, mc):
         m.replay()
         torch.cuda.synchronize()
         assert torch.equal(m.x, ref[t]), f"fused replay {t} differs"
+
+
+def test_fused_block_through_the_cache(torch_gpu, mc):
+    """Both fused launches on cache-managed experts (pinned host tensors behind LSB-tagged tables,
+    promoted into the HBM pool by the step between tokens): outputs bit-identical to the same
+    launches on device-resident copies, and the recorder counts every pick of the three tensors."""
+    torch = torch_gpu
+    import helpers as H
+    E, U, H_, F, n_tok, slots = 16, 4, 1024, 256, 2, 6
+    wt, st = mc.Q2_K, mc.Q4_K
+    mc.reset()
+    mc.configure(enabled=True, slots=slots)
+    stream = _stream(torch)
+    w_np = {r: H.weights(wt, E, F, H_, seed=40 + i) for i, r in enumerate(("gate", "up"))}
+    w_np["down"] = H.weights(wt, E, H_, F, seed=43)
+    host, dev, keep = {}, {}, []
+    for r, arr in w_np.items():
+        p = torch.empty(arr.size, dtype=torch.uint8, pin_memory=True)
+        p.numpy()[:] = arr.reshape(-1)
+        host[r], dev[r] = p, torch.from_numpy(arr).cuda()
+    t_up = mc.make_tensor(wt, H_, F, E, host["up"].data_ptr(), name="blk.0.ffn_up_exps.weight", keep=keep)
+    t_gate = mc.make_tensor(wt, H_, F, E, host["gate"].data_ptr(), name="blk.0.ffn_gate_exps.weight", keep=keep)
+    t_down = mc.make_tensor(wt, F, H_, E, host["down"].data_ptr(), name="blk.0.ffn_down_exps.weight", keep=keep)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(12)
+    md = import_module("a6000_custom_kernels_amd.moe_decode")
+    sh = {r: md.random_expert_tensor(torch, st, 1, rows, k, gen)[0]
+          for r, rows, k in (("gate", F, H_), ("up", F, H_), ("down", H_, F))}
+    rng = np.random.default_rng(31)
+    nw = torch.from_numpy(rng.uniform(0.5, 1.5, H_).astype(np.float32)).cuda()
+    ids = torch.zeros((n_tok, U), dtype=torch.int32, device="cuda")
+    w = torch.zeros((n_tok, U), dtype=torch.float32, device="cuda")
+
+    def block(use_cache, x):
+        h = torch.zeros((n_tok, U + 1, F), dtype=torch.float32, device="cuda")
+        hq = torch.zeros((n_tok, U + 1, F // 32 * 36), dtype=torch.uint8, device="cuda")
+        out = torch.zeros_like(x)
+        f_gu = mc.make_fusion(glu_op=mc.GLU_SWIGLU, shared_up=sh["up"], shared_gate=sh["gate"],
+                              shared_dst=h[:, U], shared_type=st)
+        f_gu.shared_stride_col_dst = (U + 1) * F
+        if not use_cache:
+            f_gu.gate = dev["gate"].data_ptr()
+        src_up = t_up if use_cache else mc.make_tensor(wt, H_, F, E, dev["up"].data_ptr(), keep=keep)
+        mc.check(mc.lib().ggml_hip_moe_ffn_gate_up_norm(
+            1 if use_cache else 0, C.byref(src_up), C.byref(t_gate) if use_cache else None, C.byref(f_gu),
+            x.data_ptr(), nw.data_ptr(), 1e-6, ids.data_ptr(), h.data_ptr(), H_, F, E, n_tok, U, H_,
+            (U + 1) * F, F, U, None, 0, hq.data_ptr(), (U + 1) * F // 32, F // 32, hq[:, U].data_ptr(),
+            (U + 1) * F // 32, stream), "gate_up_norm")
+        f_dn = mc.make_fusion(shared_up=sh["down"], shared_type=st, shared_src1=hq[:, U],
+                              shared_stride_col_y=(U + 1) * F // 32)
+        src_dn = t_down if use_cache else mc.make_tensor(wt, F, H_, E, dev["down"].data_ptr(), keep=keep)
+        mc.check(mc.lib().ggml_hip_moe_ffn_down_combine(
+            1 if use_cache else 0, mc.ACT_Q8_1, C.byref(src_dn), C.byref(f_dn), hq.data_ptr(), ids.data_ptr(),
+            w.data_ptr(), x.data_ptr(), out.data_ptr(), F, H_, E, n_tok, U, (U + 1) * F // 32, F // 32, H_, U,
+            stream), "down_combine")
+        return h, out
+
+    x = torch.from_numpy(rng.standard_normal((n_tok, H_)).astype(np.float32)).cuda()
+    for step in range(6):
+        ids.copy_(torch.from_numpy(np.stack([rng.choice(E, U, replace=False) for _ in range(n_tok)]).astype(np.int32)))
+        w.copy_(torch.from_numpy(rng.dirichlet(np.ones(U), n_tok).astype(np.float32)))
+        h_c, x_c = block(True, x)
+        stats = mc.stats_snapshot()
+        h_r, x_r = block(False, x)
+        torch.cuda.synchronize()
+        assert torch.equal(h_c, h_r), f"step {step}: GLU rows differ between cache and resident paths"
+        assert torch.equal(x_c, x_r), f"step {step}: residual differs between cache and resident paths"
+        assert int(stats[0]) + int(stats[1]) == 3 * n_tok * U, (step, int(stats[0]), int(stats[1]))
+        mc.step()
+        x = x_c
+    tot = mc.totals()
+    assert tot.promotions > 0 and tot.hits > 0
+    mc.reset()
