@@ -471,8 +471,12 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Streams [start, start + nbytes) of the matrix at `base` into lds (lds[x] = byte
 // (start & ~15) + x of the 16-byte aligned view); returns the number of DMA
-// instructions issued (one per KiB).
-template <int T>
+// instructions issued (one per KiB).  The destination holds whole 1 KiB rounds
+// (lanes of the last round past the span write zeros: the descriptor ends with the
+// span), or with MASK_TAIL only round_up_16(lead + nbytes) bytes: the last round is
+// then issued separately with the lanes past the span switched off (it costs the
+// plain GEMV a few percent, so only the kernels short of LDS use it).
+template <int T, bool MASK_TAIL = false>
 __device__ __forceinline__ int dma_span(const uint8_t *base, u32 base_bytes, u32 start, u32 nbytes, uint8_t *lds) {
     const uintptr_t abase = (uintptr_t) base & ~(uintptr_t) 15;
     const u32 skew = (u32) ((uintptr_t) base - abase);
@@ -485,15 +489,22 @@ __device__ __forceinline__ int dma_span(const uint8_t *base, u32 base_bytes, u32
     const int rounds = (int) ((lead + nbytes + 1023u) >> 10);
     constexpr int MAXR = span_lds_bytes(T) / 1024;
     const u32 lane_off = a0 + 16u * (threadIdx.x % WAVE);
-    // lanes of the last round past the span do not write LDS: the destination needs
-    // only round_up_16(lead + nbytes) bytes
-    const bool last_lane_on = 16u * (threadIdx.x % WAVE) < lead + nbytes - 1024u * (u32) (rounds - 1);
+    if constexpr (!MASK_TAIL) {
 #pragma unroll
-    for (int i = 0; i < MAXR; ++i) {
-        if (i < rounds) {
-            if (i < rounds - 1 || last_lane_on)
+        for (int i = 0; i < MAXR; ++i) {
+            if (i < rounds) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * i), 16, lane_off + 1024u * i, 0, 0, 0);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < MAXR; ++i) {
+            if (i < rounds - 1)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * i), 16, lane_off + 1024u * i, 0, 0, 0);
         }
+        const u32 last = (u32) (rounds - 1);
+        if (16u * (threadIdx.x % WAVE) < lead + nbytes - 1024u * last)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * last), 16, lane_off + 1024u * last, 0, 0, 0);
     }
     return rounds;
 }

@@ -198,9 +198,9 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
     if (run) {
         wait_lds_count(sync + 2, (u32) NP);                   // the prologue's loads go out first
         if (sh) {
-            if constexpr (TS != 0) step_dma<TS>(a, s, span);
+            if constexpr (TS != 0) step_dma<TS, true>(a, s, span);
         } else {
-            step_dma<TW>(a, s, span);
+            step_dma<TW, true>(a, s, span);
         }
         wait_loads_at_most(s.wgate ? s.n_up : 0);             // gate span landed (up may still land)
         run = wait_lds_count(sync + 1, (u32) NP);             // the normalized row is complete

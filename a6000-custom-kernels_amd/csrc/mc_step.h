@@ -153,8 +153,9 @@ __device__ __forceinline__ void step_resolve(const GemvArgs &a, StepCtx &s) {
     }
 }
 
-// The DMA of the gate span (to span + lds_span) and the up span (to span) of a valid step.
-template <int T>
+// The DMA of the gate span (to span + lds_span) and the up span (to span) of a valid step
+// (MASK_TAIL: dma_span's 16-byte destination sizing).
+template <int T, bool MASK_TAIL = false>
 __device__ __forceinline__ void step_dma(const GemvArgs &a, StepCtx &s, uint8_t *span) {
     constexpr TypeGeom G = type_geom(T);
     const int nu = a.ncols / G.unit_elems;
@@ -162,8 +163,8 @@ __device__ __forceinline__ void step_dma(const GemvArgs &a, StepCtx &s, uint8_t 
     const u32 mbytes = (u32) (s.shared ? a.sh_matrix_bytes : a.expert_bytes);
     s.start = (u32) s.row0 * RB;
     const u32 nbytes = (u32) s.nrows_here * RB;
-    if (s.wgate) s.n_gate = dma_span<T>(s.wgate, mbytes, s.start, nbytes, span + a.lds_span);
-    s.n_up = dma_span<T>(s.wup, mbytes, s.start, nbytes, span);
+    if (s.wgate) s.n_gate = dma_span<T, MASK_TAIL>(s.wgate, mbytes, s.start, nbytes, span + a.lds_span);
+    s.n_up = dma_span<T, MASK_TAIL>(s.wup, mbytes, s.start, nbytes, span);
 }
 
 // step_resolve, then step_dma (nothing is issued for an out-of-range expert id).
