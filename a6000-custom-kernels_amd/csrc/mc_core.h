@@ -528,6 +528,63 @@ __device__ __forceinline__ void wait_loads_at_most(int n) {
     }
 }
 
+// Cross-lane moves that stay off the LDS crossbar (which the weight DMA keeps busy):
+// DPP inside a 16-lane row, gfx950 permlane swaps across rows.
+template <int CTRL, int BANKS = 0xF>
+__device__ __forceinline__ float dpp_f(float old, float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v),
+                                                                 CTRL, 0xF, BANKS, false));
+}
+constexpr int DPP_QUAD_XOR1 = 0xB1, DPP_QUAD_XOR2 = 0x4E, DPP_ROW_SHL4 = 0x104, DPP_ROW_SHL8 = 0x108,
+              DPP_ROW_SHR4 = 0x114, DPP_ROW_SHR8 = 0x118, DPP_WAVE_SHL1 = 0x130, DPP_ROW_HALF_MIRROR = 0x141;
+
+// lanes 0..31 receive lanes 32..63 (v_permlane32_swap: the source operand's low half takes
+// the destination operand's high half)
+__device__ __forceinline__ float from_lane_plus32(float v) {
+    const u32 b = __builtin_bit_cast(u32, v);
+    return __builtin_bit_cast(float, (u32) __builtin_amdgcn_permlane32_swap(b, b, false, false)[1]);
+}
+// lanes 16g .. 16g+15 of even rows g receive the next row (v_permlane16_swap)
+__device__ __forceinline__ float from_lane_plus16(float v) {
+    const u32 b = __builtin_bit_cast(u32, v);
+    return __builtin_bit_cast(float, (u32) __builtin_amdgcn_permlane16_swap(b, b, false, false)[1]);
+}
+// lane l receives lane l ^ 4 (within 8-lane groups): row_shl:4 into banks 0 and 2, row_shr:4 into 1 and 3
+__device__ __forceinline__ float from_lane_xor4(float v) {
+    return dpp_f<DPP_ROW_SHR4, 0xA>(dpp_f<DPP_ROW_SHL4, 0x5>(v, v), v);
+}
+// lane l receives lane l ^ M
+template <int M>
+__device__ __forceinline__ float xor_lanes(float v) {
+    static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "lane xor mask");
+    if constexpr (M == 1) return dpp_f<DPP_QUAD_XOR1>(0.0f, v);
+    if constexpr (M == 2) return dpp_f<DPP_QUAD_XOR2>(0.0f, v);
+    if constexpr (M == 4) return from_lane_xor4(v);
+    if constexpr (M == 8) return dpp_f<DPP_ROW_SHR8, 0xC>(dpp_f<DPP_ROW_SHL8, 0x3>(v, v), v);
+    const u32 b = __builtin_bit_cast(u32, v);
+    const int lane = threadIdx.x % WAVE;
+    if constexpr (M == 16) {
+        // even rows take the swap's source half (the next row), odd rows its destination half
+        const auto p = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+        return __builtin_bit_cast(float, (u32) ((lane & 16) ? p[0] : p[1]));
+    }
+    const auto p = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+    return __builtin_bit_cast(float, (u32) ((lane & 32) ? p[0] : p[1]));
+}
+// xor_lanes with a mask that full unrolling makes a constant
+__device__ __forceinline__ float xor_lanes_rt(float v, int m) {
+    switch (m) {
+        case 1: return xor_lanes<1>(v);
+        case 2: return xor_lanes<2>(v);
+        case 4: return xor_lanes<4>(v);
+        case 8: return xor_lanes<8>(v);
+        case 16: return xor_lanes<16>(v);
+        default: return xor_lanes<32>(v);
+    }
+}
+// lane l receives lane l + 1 across the whole wave (DPP wave_shl:1; lane 63 keeps its value)
+__device__ __forceinline__ float wave_shl1(float v) { return dpp_f<DPP_WAVE_SHL1>(v, v); }
+
 // Uniform loads through the scalar data cache (read-only data: routing ids and
 // pointer tables, which no kernel writes while it runs).
 template <class V>
@@ -538,13 +595,23 @@ __device__ __forceinline__ V sload(const V *p) {
 // Sum over the nu consecutive lanes of each row group (lane r*nu .. r*nu+nu-1):
 // xor butterfly when nu is a power of two (total in every lane of the group),
 // else lane r*nu adds lanes r*nu+1 .. r*nu+nu-1 in order (total in lane r*nu).
+// Every exchange is a DPP move or a permlane swap (see xor_lanes / wave_shl1), so
+// the sums stay off the LDS crossbar.
 __device__ __forceinline__ float row_group_sum(float v, int nu) {
     if ((nu & (nu - 1)) == 0) {
-        for (int off = nu >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, WAVE);
+        if (nu >= 64) v += xor_lanes<32>(v);
+        if (nu >= 32) v += xor_lanes<16>(v);
+        if (nu >= 16) v += xor_lanes<8>(v);
+        if (nu >= 8) v += xor_lanes<4>(v);
+        if (nu >= 4) v += xor_lanes<2>(v);
+        if (nu >= 2) v += xor_lanes<1>(v);
         return v;
     }
-    float s = v;
-    for (int i = 1; i < nu; ++i) s += __shfl_down(v, (unsigned) i, WAVE);
+    float s = v, o = v;
+    for (int i = 1; i < nu; ++i) {
+        o = wave_shl1(o);                 // lane l: v of lane l + i
+        s += o;
+    }
     return s;
 }
 
@@ -616,8 +683,8 @@ __device__ __forceinline__ int8_t q8_1_lane(float x, float &d, float &sum) {
     sum = x;
 #pragma unroll
     for (int off = 16; off > 0; off >>= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, off, 32));
-        sum += __shfl_xor(sum, off, 32);
+        amax = fmaxf(amax, xor_lanes_rt(amax, off));
+        sum += xor_lanes_rt(sum, off);
     }
     d = amax / 127.0f;
     return amax == 0.0f ? (int8_t) 0 : (int8_t) roundf(x / d);
@@ -678,18 +745,21 @@ __device__ __forceinline__ void quantize_row_lds(const float *x, uint8_t *q, int
 }
 
 // Sum of squares of one 256-value chunk in the canonical RMS order (mc_internal.h):
-// lane l holds values 4l .. 4l+3 of the chunk in xv; returned in every lane.
+// lane l holds values 4l .. 4l+3 of the chunk in xv; returned in every lane.  The
+// shuffle-down tree (offsets 32 .. 1, lane l < off adds lane l + off) runs on permlane
+// swaps and DPP: lane 0's operands at every level are exactly the tree's (the other
+// lanes' values are not used).
 __device__ __forceinline__ float rms_chunk_sum(const float xv[4]) {
-    const int lane = threadIdx.x % WAVE;
     float a = 0.0f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) a = fmaf(xv[k], xv[k], a);
-#pragma unroll
-    for (int off = WAVE / 2; off > 0; off >>= 1) {
-        const float other = __shfl_down(a, off, WAVE);
-        if (lane < off) a += other;
-    }
-    return __shfl(a, 0, WAVE);
+    a += from_lane_plus32(a);
+    a += from_lane_plus16(a);
+    a += dpp_f<DPP_ROW_SHL8>(0.0f, a);
+    a += dpp_f<DPP_ROW_SHL4>(0.0f, a);
+    a += dpp_f<DPP_QUAD_XOR2>(0.0f, a);
+    a += dpp_f<DPP_QUAD_XOR1>(0.0f, a);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 0));
 }
 
 constexpr int COMBINE_MAX_USED = 16;
@@ -736,13 +806,13 @@ __device__ __forceinline__ float combine_chunk(const float *o, int64_t o_stride,
     return rms_chunk_sum(xv);
 }
 
-// Maximum over the 8-lane group of each lane (lanes 8g .. 8g+7): quad exchanges by DPP,
-// the exchange between the two quads of the group by ds_swizzle (xor 4).  fmaxf is exact,
-// so the result equals any other reduction order.
+// Maximum over the 8-lane group of each lane (lanes 8g .. 8g+7), all by DPP: the two quad
+// exchanges, then the mirror inside the half-row (which pairs each quad with the other
+// quad of its group).  fmaxf is exact, so the result equals any other reduction order.
 __device__ __forceinline__ float max8(float v) {
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x101F)));
+    v = fmaxf(v, dpp_f<DPP_QUAD_XOR1>(0.0f, v));
+    v = fmaxf(v, dpp_f<DPP_QUAD_XOR2>(0.0f, v));
+    v = fmaxf(v, dpp_f<DPP_ROW_HALF_MIRROR>(0.0f, v));
     return v;
 }
 
@@ -753,7 +823,8 @@ __device__ __forceinline__ float max8(float v) {
 // code = amax == 0 ? 0 : roundf(v / d), and the block sum in the quantizer's
 // xor-butterfly order (offsets 16, 8, 4 across lanes, then 2, 1 inside the lane).
 // WITH_SUM = false leaves the sum field 0: the K-quant dots read only d and the codes.
-template <bool WITH_SUM = true>
+// S16: also the 16-value code sums of the chunk into s16[16 j ..].
+template <bool WITH_SUM = true, bool S16 = false>
 __device__ __forceinline__ void quantize_chunk(const float xv[4], bool norm, float s, const v4f nwv, uint8_t *y,
                                                int j, int16_t *s16 = nullptr) {
     const int lane = threadIdx.x % WAVE;
@@ -770,7 +841,11 @@ __device__ __forceinline__ void quantize_chunk(const float xv[4], bool norm, flo
 #pragma unroll
         for (int off = 4; off > 0; off >>= 1) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) t[k] += __shfl_xor(t[k], off, WAVE);
+            for (int k = 0; k < 4; ++k) {
+                const float o = off == 4 ? from_lane_xor4(t[k])
+                                         : off == 2 ? dpp_f<DPP_QUAD_XOR2>(0.0f, t[k]) : dpp_f<DPP_QUAD_XOR1>(0.0f, t[k]);
+                t[k] += o;
+            }
         }
         const float t2[4] = {t[0] + t[2], t[1] + t[3], t[2] + t[0], t[3] + t[1]};
         sum = t2[0] + t2[1];
@@ -791,7 +866,7 @@ __device__ __forceinline__ void quantize_chunk(const float xv[4], bool norm, flo
     *(u32 *) (yb + 4 + (i % 32)) = packed;
     // the eight lanes of a block store the same scale word (no branch around the store)
     *(u32 *) yb = (u32) f2h_bits(d) | (WITH_SUM ? ((u32) f2h_bits(sum) << 16) : 0u);
-    if (s16) {
+    if constexpr (S16) {
         // sums of each 16 codes of the chunk (lanes 4m .. 4m+3 hold sub-block m): quad sums by DPP
         int cs = sdot4(packed, 0x01010101u, 0);
         cs += __builtin_amdgcn_update_dpp(0, cs, 0xB1, 0xF, 0xF, false);

@@ -99,7 +99,7 @@ __device__ __forceinline__ void gu_prologue(const GemvArgs &a, int t, int p, flo
 #pragma unroll
     for (int ci = 0; ci < PC; ++ci) {
         const float x4[4] = {xv[ci].x, xv[ci].y, xv[ci].z, xv[ci].w};
-        quantize_chunk<false>(x4, true, scale, nwv[ci], ys, min(p + NP * ci, nchunk - 1), s16);
+        quantize_chunk<false, true>(x4, true, scale, nwv[ci], ys, min(p + NP * ci, nchunk - 1), s16);
     }
     if (write_y_out) {
 #pragma unroll

@@ -108,8 +108,8 @@ __global__ __launch_bounds__(256) void mc_quantize_q8_1_kernel(const QuantArgs a
     float amax = fabsf(x), sum = x;
 #pragma unroll
     for (int off = 16; off > 0; off >>= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, off, 32));
-        sum += __shfl_xor(sum, off, 32);
+        amax = fmaxf(amax, xor_lanes_rt(amax, off));
+        sum += xor_lanes_rt(sum, off);
     }
     if (!valid) return;
     const float d = amax / 127.0f;
@@ -133,7 +133,7 @@ __global__ __launch_bounds__(256) void mc_quantize_q8_0_as_q8_1_kernel(const Qua
     const float x = valid ? a.x[row * a.x_stride + b * 32 + l] : 0.0f;
     float amax = fabsf(x);
 #pragma unroll
-    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, xor_lanes_rt(amax, off));
     if (!valid) return;
     const float d = amax / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
