@@ -32,6 +32,21 @@ __device__ __forceinline__ int sdot4(u32 a, u32 b, int c) {
 
 __device__ __forceinline__ u32 byte_of(u32 w, int i) { return (w >> (8 * i)) & 0xFFu; }
 
+// a . b over four int8 lanes with no accumulator (the VOP3 form takes the constant 0,
+// where the accumulating form would need a zeroed register first)
+__device__ __forceinline__ int sdot4_z(u32 a, u32 b) {
+    int r;
+    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+// a . b over two int16 lanes, no accumulator
+__device__ __forceinline__ int sdot2_z(u32 a, u32 b) {
+    int r;
+    asm("v_dot2_i32_i16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, u32 nbytes) {
     // gfx9 raw buffer: stride 0, num_records in bytes, dword3 = 0x00020000
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short) 0, (int) nbytes, 0x00020000);
@@ -50,6 +65,7 @@ struct Act {
     u32 q[UE / 4];
     float d[UE / 32];
     int s16[UE / 16];
+    u32 s2[UE / 32];             // s16[2i] | s16[2i+1] << 16 (int16 lanes)
 };
 
 // Sums of each 16 int8 activation values (the min/offset terms of the dots).
@@ -62,6 +78,8 @@ __device__ __forceinline__ void act_sums(Act<UE> &A) {
         t = sdot4(A.q[4 * s + 2], 0x01010101u, t);
         A.s16[s] = sdot4(A.q[4 * s + 3], 0x01010101u, t);
     }
+#pragma unroll
+    for (int i = 0; i < UE / 32; ++i) A.s2[i] = ((u32) A.s16[2 * i] & 0xFFFFu) | ((u32) A.s16[2 * i + 1] << 16);
 }
 
 typedef u32 v4u __attribute__((ext_vector_type(4)));
@@ -111,6 +129,7 @@ __device__ __forceinline__ void load_act_lds(Act<UE> &A, const uint8_t *p, const
 #pragma unroll
         for (int i = 0; i < UE / 32; ++i) {
             const u32 pair = sw[i];
+            A.s2[i] = pair;
             A.s16[2 * i] = (int) (int16_t) (pair & 0xFFFFu);
             A.s16[2 * i + 1] = (int) (int16_t) (pair >> 16);
         }
@@ -168,13 +187,19 @@ struct WordsShifted {            // unit starts on a 2-byte boundary: realign wi
 
 // Q2_K: scales[16] | qs[64] | d | dmin.  Element i = 128h + 32j + l uses
 // (qs[32h + l] >> 2j) & 3 and sub-block scale byte i >> 4 (lo 4: scale, hi 4: min).
+// The 2-bit fields of j < 3 stay in place (value * 4^j): the factor 4^-j is folded
+// into the activation scale (exact, a power of two).  The min term of each 32-value
+// group is one v_dot2 of the two 4-bit mins (int16 lanes) with the packed 16-value sums.
 template <int ACT, class W>
 __device__ __forceinline__ float dot_q2_K(const W &w, const Act<256> &A) {
     const u32 dm = w[20];
     const float d = h2f(dm), dmin = h2f(dm >> 16);
-    u32 sc[4];
+    u32 sc[4], mh[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sc[i] = w[i];
+    for (int i = 0; i < 4; ++i) {
+        sc[i] = w[i];
+        mh[i] = (sc[i] >> 4) & 0x0F0F0F0Fu;
+    }
     float accI = 0.0f, accM = 0.0f;
     int isum = 0, msum = 0;
 #pragma unroll
@@ -192,19 +217,20 @@ __device__ __forceinline__ float dot_q2_K(const W &w, const Act<256> &A) {
             for (int k = 0; k < 4; ++k) {
                 const u32 v0 = j < 3 ? (q[k] & (0x03030303u << (2 * j))) : ((q[k] >> 6) & 0x03030303u);
                 const u32 v1 = j < 3 ? (q[k + 4] & (0x03030303u << (2 * j))) : ((q[k + 4] >> 6) & 0x03030303u);
-                d0 = sdot4(v0, A.q[8 * g + k], d0);
-                d1 = sdot4(v1, A.q[8 * g + 4 + k], d1);
+                d0 = k == 0 ? sdot4_z(v0, A.q[8 * g + k]) : sdot4(v0, A.q[8 * g + k], d0);
+                d1 = k == 0 ? sdot4_z(v1, A.q[8 * g + 4 + k]) : sdot4(v1, A.q[8 * g + 4 + k], d1);
             }
-            const u32 b0 = byte_of(sc[(2 * g) >> 2], (2 * g) & 3);
-            const u32 b1 = byte_of(sc[(2 * g + 1) >> 2], (2 * g + 1) & 3);
-            const int is = __mul24((int) (b0 & 0xF), d0) + __mul24((int) (b1 & 0xF), d1);
-            const int ms = __mul24((int) (b0 >> 4), A.s16[2 * g]) + __mul24((int) (b1 >> 4), A.s16[2 * g + 1]);
+            const int kb = 2 * (g & 1);                   // scale bytes 2g, 2g+1 of word g / 2
+            const u32 wsc = sc[g >> 1];
+            const int is = __mul24((int) ((wsc >> (8 * kb)) & 0xFu), d0) + __mul24((int) ((wsc >> (8 * kb + 8)) & 0xFu), d1);
+            const u32 mp = __builtin_amdgcn_perm(0u, mh[g >> 1], kb == 0 ? 0x0C010C00u : 0x0C030C02u);
+            const int ms = sdot2_z(mp, A.s2[g]);
             if constexpr (ACT == ACT_Q8_K) {
                 isum += is >> (2 * jj);
                 msum += ms;
             } else {
-                const float fi = (float) is * (jj == 0 ? 1.0f : (jj == 1 ? 0.25f : 0.0625f));
-                accI = fmaf(A.d[g], fi, accI);
+                const float dj = jj == 0 ? A.d[g] : A.d[g] * (jj == 1 ? 0.25f : 0.0625f);
+                accI = fmaf(dj, (float) is, accI);
                 accM = fmaf(A.d[g], (float) ms, accM);
             }
         }
@@ -872,6 +898,89 @@ __device__ __forceinline__ void quantize_chunk(const float xv[4], bool norm, flo
         cs += __builtin_amdgcn_update_dpp(0, cs, 0xB1, 0xF, 0xF, false);
         cs += __builtin_amdgcn_update_dpp(0, cs, 0x4E, 0xF, 0xF, false);
         s16[16 * j + lane / 4] = (int16_t) cs;    // the four lanes of a quad store the same value
+    }
+}
+
+// The same arithmetic for N chunks of one wave, written stage by stage so that the N
+// dependency chains (cross-lane steps, divisions) interleave instead of running one
+// after another.  rms_chunk_sums = rms_chunk_sum per chunk; quantize_chunks =
+// quantize_chunk<false, true> per chunk under norm (chunk index j[i]).
+template <int N>
+__device__ __forceinline__ void rms_chunk_sums(const v4f xv[N], float out[N]) {
+    float a[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        a[i] = fmaf(xv[i].x, xv[i].x, 0.0f);
+        a[i] = fmaf(xv[i].y, xv[i].y, a[i]);
+        a[i] = fmaf(xv[i].z, xv[i].z, a[i]);
+        a[i] = fmaf(xv[i].w, xv[i].w, a[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) a[i] += from_lane_plus32(a[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) a[i] += from_lane_plus16(a[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) a[i] += dpp_f<DPP_ROW_SHL8>(0.0f, a[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) a[i] += dpp_f<DPP_ROW_SHL4>(0.0f, a[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) a[i] += dpp_f<DPP_QUAD_XOR2>(0.0f, a[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) a[i] += dpp_f<DPP_QUAD_XOR1>(0.0f, a[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a[i]), 0));
+}
+
+template <int N>
+__device__ __forceinline__ void quantize_chunks(const v4f xv[N], const v4f nwv[N], float s, uint8_t *y, const int j[N],
+                                                int16_t *s16) {
+    const int lane = threadIdx.x % WAVE;
+    float v[N][4], amax[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        v[i][0] = (xv[i].x * s) * nwv[i].x;
+        v[i][1] = (xv[i].y * s) * nwv[i].y;
+        v[i][2] = (xv[i].z * s) * nwv[i].z;
+        v[i][3] = (xv[i].w * s) * nwv[i].w;
+        amax[i] = fmaxf(fmaxf(fabsf(v[i][0]), fabsf(v[i][1])), fmaxf(fabsf(v[i][2]), fabsf(v[i][3])));
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) amax[i] = fmaxf(amax[i], dpp_f<DPP_QUAD_XOR1>(0.0f, amax[i]));
+#pragma unroll
+    for (int i = 0; i < N; ++i) amax[i] = fmaxf(amax[i], dpp_f<DPP_QUAD_XOR2>(0.0f, amax[i]));
+#pragma unroll
+    for (int i = 0; i < N; ++i) amax[i] = fmaxf(amax[i], dpp_f<DPP_ROW_HALF_MIRROR>(0.0f, amax[i]));
+    float d[N], dq[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        d[i] = amax[i] / 127.0f;
+        dq[i] = amax[i] == 0.0f ? 1.0f : d[i];
+    }
+    u32 packed[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        packed[i] = 0u;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int q = (int) roundf(v[i][k] / dq[i]);
+            const int code = amax[i] == 0.0f ? 0 : q;
+            packed[i] |= ((u32) code & 0xFFu) << (8 * k);
+        }
+    }
+    int cs[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) cs[i] = sdot4(packed[i], 0x01010101u, 0);
+#pragma unroll
+    for (int i = 0; i < N; ++i) cs[i] += __builtin_amdgcn_update_dpp(0, cs[i], DPP_QUAD_XOR1, 0xF, 0xF, false);
+#pragma unroll
+    for (int i = 0; i < N; ++i) cs[i] += __builtin_amdgcn_update_dpp(0, cs[i], DPP_QUAD_XOR2, 0xF, 0xF, false);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const int e = j[i] * RMS_CHUNK + 4 * lane;
+        uint8_t *yb = y + (e / 32) * 36;
+        *(u32 *) (yb + 4 + (e % 32)) = packed[i];
+        *(u32 *) yb = (u32) f2h_bits(d[i]);
+        s16[16 * j[i] + lane / 4] = (int16_t) cs[i];
     }
 }
 

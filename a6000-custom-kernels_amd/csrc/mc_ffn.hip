@@ -81,11 +81,7 @@ __device__ __forceinline__ void gu_prologue(const GemvArgs &a, int t, int p, flo
     }
     if (lane == 0) __hip_atomic_fetch_add(sync + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     float cs[PC];
-#pragma unroll
-    for (int ci = 0; ci < PC; ++ci) {
-        const float x4[4] = {xv[ci].x, xv[ci].y, xv[ci].z, xv[ci].w};
-        cs[ci] = rms_chunk_sum(x4);
-    }
+    rms_chunk_sums<PC>(xv, cs);
     if (lane == 0) {
 #pragma unroll
         for (int ci = 0; ci < PC; ++ci) red[min(p + NP * ci, nchunk - 1)] = cs[ci];
@@ -94,13 +90,14 @@ __device__ __forceinline__ void gu_prologue(const GemvArgs &a, int t, int p, flo
     if (lane == 0) __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     wait_lds_count(sync, (u32) NP);
     float ss = 0.0f;                                          // ascending, as every other producer of y
-    for (int j = 0; j < nchunk; ++j) ss += red[j];
-    const float scale = 1.0f / sqrtf(ss / (float) K + a.eps);
 #pragma unroll
-    for (int ci = 0; ci < PC; ++ci) {
-        const float x4[4] = {xv[ci].x, xv[ci].y, xv[ci].z, xv[ci].w};
-        quantize_chunk<false, true>(x4, true, scale, nwv[ci], ys, min(p + NP * ci, nchunk - 1), s16);
-    }
+    for (int j = 0; j < NP * PC; ++j)
+        if (j < nchunk) ss += red[j];
+    const float scale = 1.0f / sqrtf(ss / (float) K + a.eps);
+    int jc[PC];
+#pragma unroll
+    for (int ci = 0; ci < PC; ++ci) jc[ci] = min(p + NP * ci, nchunk - 1);
+    quantize_chunks<PC>(xv, nwv, scale, ys, jc, s16);
     if (write_y_out) {
 #pragma unroll
         for (int ci = 0; ci < PC; ++ci) {
