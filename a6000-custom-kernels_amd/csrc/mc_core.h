@@ -89,7 +89,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 // 36 bytes, or one 292-byte q8_K block, at p (4-byte aligned).  When p is 16-byte
 // aligned (q8_1 slices of 256 values are 288 bytes: 18 chunks) the slice is read
 // with 128-bit LDS reads, else with 32-bit reads.
-template <int UE, int ACT>
+template <int UE, int ACT, bool S16 = false>
 __device__ __forceinline__ void load_act_lds(Act<UE> &A, const uint8_t *p, const int16_t *s16 = nullptr) {
     constexpr int NW = ACT == ACT_Q8_1 ? UE / 32 * 9 : 73;
     u32 w[NW];
@@ -123,7 +123,7 @@ __device__ __forceinline__ void load_act_lds(Act<UE> &A, const uint8_t *p, const
 #pragma unroll
         for (int k = 0; k < 64; ++k) A.q[k] = w[1 + k];
     }
-    if (s16) {
+    if constexpr (S16) {
         // the 16-value sums precomputed next to the row (exact integer sums of the same codes)
         const u32 *sw = (const u32 *) s16;
 #pragma unroll
@@ -899,6 +899,23 @@ __device__ __forceinline__ void quantize_chunk(const float xv[4], bool norm, flo
         cs += __builtin_amdgcn_update_dpp(0, cs, 0x4E, 0xF, 0xF, false);
         s16[16 * j + lane / 4] = (int16_t) cs;    // the four lanes of a quad store the same value
     }
+}
+
+// 16-value sums of the codes of a q8_1 row of k values in LDS (36-byte blocks from p,
+// 4-byte aligned) into s16[0 .. k/16): sum i covers codes 16i .. 16i+15, one sum per
+// lane and pass.  These are the integers act_sums forms for each unit of the row, so
+// a wave computes them once instead of every lane of a unit column repeating them.
+__device__ __forceinline__ void row_sums16_lds(const uint8_t *p, int k, int16_t *s16) {
+    const int lane = threadIdx.x % WAVE;
+    for (int i = lane; i < k / 16; i += WAVE) {
+        const u32 *q = (const u32 *) (p + (i >> 1) * 36 + 4 + 16 * (i & 1));
+        int t = sdot4(q[0], 0x01010101u, 0);
+        t = sdot4(q[1], 0x01010101u, t);
+        t = sdot4(q[2], 0x01010101u, t);
+        t = sdot4(q[3], 0x01010101u, t);
+        s16[i] = (int16_t) t;
+    }
+    asm volatile("" ::: "memory");    // the wave's LDS writes stay ahead of its reads
 }
 
 // The same arithmetic for N chunks of one wave, written stage by stage so that the N

@@ -208,11 +208,11 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
         float su, sg;
         if (sh) {
             if constexpr (TS != 0) {
-                step_dots<TS, ACT_Q8_1>(a, s, span, ys, su, sg, s16);
+                step_dots<TS, ACT_Q8_1, true>(a, s, span, ys, su, sg, s16);
                 rl = step_store<TS>(a, s, su, sg, v);
             }
         } else {
-            step_dots<TW, ACT_Q8_1>(a, s, span, ys, su, sg, s16);
+            step_dots<TW, ACT_Q8_1, true>(a, s, span, ys, su, sg, s16);
             rl = step_store<TW>(a, s, su, sg, v);
         }
     }
@@ -222,7 +222,7 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
 // ---------------------------------------------------------------------------
 // down projection + combine
 // ---------------------------------------------------------------------------
-// Dynamic LDS: [nwaves x (span | activation staging | q8_1 row)] [row results nwaves x rps]
+// Dynamic LDS: [nwaves x (span | activation staging | q8_1 row | 16-value sums)] [row results nwaves x rps]
 template <int TW, int TS, int ACT>
 __global__ __launch_bounds__(FFN_DN_MAX_WAVES *WAVE) void mc_ffn_down_combine_kernel(const GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -271,15 +271,19 @@ __global__ __launch_bounds__(FFN_DN_MAX_WAVES *WAVE) void mc_ffn_down_combine_ke
             quantize_row_lds((const float *) arow, span + a.lds_q8, a.ncols);
             arow = span + a.lds_q8;
         }
+        // the row's 16-value code sums, once per wave (the K-quant dots' min terms)
+        static_assert(AQ == ACT_Q8_1, "down + combine reads q8_1 rows");
+        int16_t *rs16 = (int16_t *) (span + a.lds_sums);
+        row_sums16_lds(arow, a.ncols, rs16);
         float su = 0.0f, sg = 0.0f;
         if (sh) {
             if constexpr (TS != 0) {
-                step_dots<TS, AQ>(a, s, span, arow, su, sg);
+                step_dots<TS, AQ, true>(a, s, span, arow, su, sg, rs16);
                 nu = a.ncols / type_geom(TS).unit_elems;
             }
             v = su;
         } else {
-            step_dots<TW, AQ>(a, s, span, arow, su, sg);
+            step_dots<TW, AQ, true>(a, s, span, arow, su, sg, rs16);
             nu = a.ncols / type_geom(TW).unit_elems;
             const int rl = lane / nu;
             v = routed_value(a, s, s.row0 + (rl < s.nrows_here ? rl : 0), su, sg);
@@ -425,7 +429,8 @@ static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act) {
         a.lds_span = sr > ss ? sr : ss;
         a.lds_act = a.lds_span;
         a.lds_q8 = a.lds_act + round_up_1k(a.act_row_bytes + 20u);
-        a.lds_wave = a.lds_q8 + q8_bytes;
+        a.lds_sums = a.lds_q8 + q8_bytes;
+        a.lds_wave = a.lds_sums + round16(2u * (uint32_t) (a.ncols / 16));
         a.lds_part = (uint32_t) a.nwaves * a.lds_wave;
         a.lds_total = a.lds_part + 4u * (uint32_t) (a.nwaves * rps);
         if (a.lds_total <= FFN_LDS_MAX) break;

@@ -136,6 +136,7 @@ struct GemvArgs {
     int32_t tiles_per_tok;        // steps per token: shared tiles first, then the routed picks'
     uint32_t lds_wave;            // LDS bytes of one wave's region (spans, activation staging)
     uint32_t lds_y;               // FFN_GATE_UP_NORM: q8_1 row
+    uint32_t lds_sums;            // FFN_DOWN_COMBINE: offset in a wave's region of its row's 16-value sums
     uint32_t lds_part;            // FFN_GATE_UP_NORM: counters + chunk sums; FFN_DOWN_COMBINE: row results [nwaves][rps]
     // FFN_GATE_UP_NORM: y = q8_1((x * rms_scale(x)) * nw), computed by every workgroup
     const float *nx;              // [n_tok][nx_stride] rows to normalize

@@ -178,7 +178,7 @@ __device__ __forceinline__ void step_issue(const GemvArgs &a, StepCtx &s, uint8_
 // blocks) is in LDS at arow and, when there is a gate, the gate span has landed
 // (the caller waited for at most n_up outstanding loads); the up span is waited
 // for here.  Returns the row sums (valid in lane row_local * nu of each row).
-template <int T, int AQ>
+template <int T, int AQ, bool S16 = false>
 __device__ __forceinline__ void step_dots(const GemvArgs &a, const StepCtx &s, const uint8_t *span,
                                           const uint8_t *arow, float &su, float &sg, const int16_t *s16 = nullptr) {
     constexpr TypeGeom G = type_geom(T);
@@ -193,10 +193,10 @@ __device__ __forceinline__ void step_dots(const GemvArgs &a, const StepCtx &s, c
     Act<UE> A;
     float pu = 0.0f, pg = 0.0f;
     // precomputed 16-value activation sums of the unit, when the caller has them (K-quant units)
-    const int16_t *us16 = s16 ? s16 + (u32) col * (UE / 16) : nullptr;
+    const int16_t *us16 = S16 ? s16 + (u32) col * (UE / 16) : nullptr;
     if (s.wgate) {
         if (active) {
-            load_act_lds<UE, AQ>(A, aslice, us16);
+            load_act_lds<UE, AQ, S16>(A, aslice, us16);
             pg = span_unit_dot<T, AQ>(span + a.lds_span, span_lead(s.wgate, s.start), unit, A);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -204,7 +204,7 @@ __device__ __forceinline__ void step_dots(const GemvArgs &a, const StepCtx &s, c
     } else {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         if (active) {
-            load_act_lds<UE, AQ>(A, aslice, us16);
+            load_act_lds<UE, AQ, S16>(A, aslice, us16);
             pu = span_unit_dot<T, AQ>(span, span_lead(s.wup, s.start), unit, A);
         }
     }
