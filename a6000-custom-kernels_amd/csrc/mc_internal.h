@@ -127,7 +127,6 @@ struct GemvArgs {
     uint32_t lds_span;            // LDS bytes per staged matrix span (up at 0, gate at lds_span)
     uint32_t lds_act;             // LDS offset of the staged activation row
     uint32_t lds_q8;              // LDS offset of the in-kernel q8_1 copy of an fp32 activation row
-    uint32_t lds_red;             // LDS offset of the 64-float reduction scratch
     uint32_t lds_total;           // dynamic LDS bytes per workgroup
     // fused decode kernels (mc_ffn.hip); FFN_NONE: the plain MUL_MAT_ID GEMV
     int32_t mode;
@@ -136,7 +135,7 @@ struct GemvArgs {
     int32_t tiles_per_tok;        // steps per token: shared tiles first, then the routed picks'
     uint32_t lds_wave;            // LDS bytes of one wave's region (spans, activation staging)
     uint32_t lds_y;               // FFN_GATE_UP_NORM: q8_1 row
-    uint32_t lds_sums;            // FFN_DOWN_COMBINE: offset in a wave's region of its row's 16-value sums
+    uint32_t lds_sums;            // LDS offset of the activation row's 16-value sums (down + combine: in a wave's region)
     uint32_t lds_part;            // FFN_GATE_UP_NORM: counters + chunk sums; FFN_DOWN_COMBINE: row results [nwaves][rps]
     // FFN_GATE_UP_NORM: y = q8_1((x * rms_scale(x)) * nw), computed by every workgroup
     const float *nx;              // [n_tok][nx_stride] rows to normalize

@@ -67,13 +67,20 @@ __device__ __forceinline__ void run_step(const GemvArgs &a, uint8_t *lds, bool s
         arow = lds + a.lds_q8;
     }
     float su, sg;
-    step_dots<T, AQ>(a, s, lds, arow, su, sg);
+    if constexpr (AQ == ACT_Q8_1) {
+        // the row's 16-value code sums, once per wave (min / offset terms of the dots)
+        int16_t *rs16 = (int16_t *) (lds + a.lds_sums);
+        row_sums16_lds(arow, a.ncols, rs16);
+        step_dots<T, AQ, true>(a, s, lds, arow, su, sg, rs16);
+    } else {
+        step_dots<T, AQ>(a, s, lds, arow, su, sg);
+    }
     step_store<T>(a, s, su, sg);
 }
 
 // One wave per workgroup.  Workgroup 0 is the pick recorder when anything is
 // recorded; then the shared-expert steps (the heaviest, dispatched first), then
-// the routed steps.  Dynamic LDS: [up span | gate span | activation row | scratch].
+// the routed steps.  Dynamic LDS: [up span | gate span | activation row | 16-value sums].
 template <int TW, int TS, int ACT>
 __global__ __launch_bounds__(WAVE) void mc_gemv_kernel(const GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -305,7 +312,7 @@ static hipError_t launch_act(const GemvArgs &a, int ts, int act, hipStream_t s) 
 // activation row.
 static int fit_rows_per_step(int nu, uint32_t row_bytes, int nspan, uint32_t act_span) {
     int r = WAVE / nu;
-    while (r > 1 && nspan * span_bytes((uint32_t) r, row_bytes) + act_span + 256u > GEMV_LDS_BUDGET) --r;
+    while (r > 1 && nspan * span_bytes((uint32_t) r, row_bytes) + act_span > GEMV_LDS_BUDGET) --r;
     return r;
 }
 
@@ -321,7 +328,9 @@ int launch_gemv(GemvArgs a, int tw, int ts, int act, void *stream) {
                     : act == ACT_Q8_K ? (uint32_t) (a.ncols / 256 * 292) : (uint32_t) a.ncols * 4u;
     // fp32 rows also need room for their q8_1 copy
     const uint32_t q8_bytes = act == ACT_F32 ? ((uint32_t) (a.ncols / 32 * 36) + 15u) & ~15u : 0u;
-    const uint32_t act_span = round_up_1k(a.act_row_bytes + 20u) + q8_bytes;
+    // q8_1 rows (given or made from fp32) also get their 16-value sums
+    const uint32_t sums_bytes = act == ACT_Q8_K ? 0u : ((uint32_t) (a.ncols / 8) + 15u) & ~15u;
+    const uint32_t act_span = round_up_1k(a.act_row_bytes + 20u) + q8_bytes + sums_bytes;
     if (ts == 0 || !a.sh_up) ts = 0;
     const int nspan = (a.has_gate || (ts != 0 && a.sh_gate)) ? 2 : 1;
     a.rps = fit_rows_per_step(nu, rb, nspan, act_span);
@@ -341,9 +350,9 @@ int launch_gemv(GemvArgs a, int tw, int ts, int act, void *stream) {
     }
     a.lds_span = span;
     a.lds_act = (uint32_t) nspan * span;
-    a.lds_q8 = a.lds_act + act_span - q8_bytes;
-    a.lds_red = a.lds_act + act_span;
-    a.lds_total = a.lds_red + 256u;
+    a.lds_q8 = a.lds_act + act_span - q8_bytes - sums_bytes;
+    a.lds_sums = a.lds_act + act_span - sums_bytes;
+    a.lds_total = a.lds_act + act_span;
     a.rec = (a.stats || a.stamps || a.stamps_gate) ? 1 : 0;
     a.n_tiles = a.n_routed_tiles + a.sh_tiles_per_tok * a.n_tok;
     if (a.n_tiles <= 0) return (int) hipSuccess;
