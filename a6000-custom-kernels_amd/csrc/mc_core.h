@@ -611,6 +611,12 @@ __device__ __forceinline__ float xor_lanes_rt(float v, int m) {
 // lane l receives lane l + 1 across the whole wave (DPP wave_shl:1; lane 63 keeps its value)
 __device__ __forceinline__ float wave_shl1(float v) { return dpp_f<DPP_WAVE_SHL1>(v, v); }
 
+// Workgroup barrier for data exchanged through LDS (ordinary LDS writes, or DMA
+// writes each wave has already waited for with its own vmcnt): unlike
+// __syncthreads(), whose release fence drains every outstanding load, it leaves
+// the buffer->LDS DMAs still in flight (the next stage of a pipeline) alone.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Uniform loads through the scalar data cache (read-only data: routing ids and
 // pointer tables, which no kernel writes while it runs).
 template <class V>

@@ -38,10 +38,6 @@
 
 namespace mc {
 
-// Workgroup barrier for data exchanged through LDS by ordinary LDS writes;
-// weight DMAs still in flight are not waited for.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 // ---------------------------------------------------------------------------
 // gate/up with the RMSNorm + q8_1 prologue
 // ---------------------------------------------------------------------------

@@ -361,12 +361,12 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
             } else {
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             }
-            __syncthreads();                                  // ... and for every wave
+            lds_barrier();                                    // ... and for every wave (stage s + 1 stays in flight)
             const uint8_t *st = lds + (uint32_t) (s & 1) * stage;
             const uint8_t *recs = st + (GATE ? 2 : 1) * WT;
             const uint32_t roff = (uint32_t) (16 * wave + lane % 16) * SBB;
             mmq_superblock<T, GATE>(st + roff, st + WT + roff, recs, nb, acc, accg);
-            __syncthreads();                                  // stage s is free for s + 2
+            lds_barrier();                                    // stage s is free for s + 2
         }
         // scatter: pair 4 (lane / 16) + i of each block, weight row lane % 16 of the wave's tile
         const int row = row0 + 16 * wave + lane % 16;
