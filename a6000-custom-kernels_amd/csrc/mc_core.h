@@ -47,6 +47,12 @@ __device__ __forceinline__ int sdot2_z(u32 a, u32 b) {
     return r;
 }
 
+typedef short v2i16 __attribute__((ext_vector_type(2)));
+// c + a . b over two int16 lanes
+__device__ __forceinline__ int sdot2(u32 a, u32 b, int c) {
+    return __builtin_amdgcn_sdot2(__builtin_bit_cast(v2i16, a), __builtin_bit_cast(v2i16, b), c, false);
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, u32 nbytes) {
     // gfx9 raw buffer: stride 0, num_records in bytes, dword3 = 0x00020000
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short) 0, (int) nbytes, 0x00020000);

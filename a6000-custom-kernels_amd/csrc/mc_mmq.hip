@@ -264,17 +264,22 @@ __device__ __forceinline__ void mmq_mfma_pair(long a_lo, long a_hi, long b_lo, l
     for (int i = 0; i < 4; ++i) isum[i] += __mul24(sl, rl[i]) + __mul24(sh, rh[i]);
 }
 
-// Sum of the eight sub-block mins (bytes of M0, M1) times a pair's 32-value code
-// sums (eight int16 in s4).
-__device__ __forceinline__ int mins_dot(u32 M0, u32 M1, const v4u s4) {
-    const u32 sw[4] = {s4.x, s4.y, s4.z, s4.w};
-    int r = 0;
-#pragma unroll
-    for (int g = 0; g < 8; ++g) {
-        const int sv = (int) (int16_t) (sw[g >> 1] >> (16 * (g & 1)));
-        r += __mul24((int) byte_of(g < 4 ? M0 : M1, g & 3), sv);
-    }
-    return r;
+// The eight sub-block mins (bytes of M0, M1) as int16 pairs (m_2k, m_2k+1), the
+// layout of a record's 32-value code sums.
+__device__ __forceinline__ void mins_pairs(u32 M0, u32 M1, u32 (&mp)[4]) {
+    mp[0] = __builtin_amdgcn_perm(0u, M0, 0x0C010C00u);
+    mp[1] = __builtin_amdgcn_perm(0u, M0, 0x0C030C02u);
+    mp[2] = __builtin_amdgcn_perm(0u, M1, 0x0C010C00u);
+    mp[3] = __builtin_amdgcn_perm(0u, M1, 0x0C030C02u);
+}
+
+// Sum of the eight sub-block mins times a pair's 32-value code sums (eight int16 in
+// s4, sub-blocks 2k and 2k+1 in word k): four v_dot2 (exact integers).
+__device__ __forceinline__ int mins_dot(const u32 (&mp)[4], const v4u s4) {
+    int r = sdot2_z(mp[0], s4.x);
+    r = sdot2(mp[1], s4.y, r);
+    r = sdot2(mp[2], s4.z, r);
+    return sdot2(mp[3], s4.w, r);
 }
 
 // One super-block of one 16-row weight tile (the wave's rows, the lane's row =
@@ -291,6 +296,9 @@ __device__ __forceinline__ void mmq_superblock(const uint8_t *wrow_up, const uin
     const RowScales su = row_scales(wu);
     RowScales sg{};
     if constexpr (GATE) sg = row_scales(wg);
+    u32 mpu[4], mpg[4] = {0u, 0u, 0u, 0u};
+    mins_pairs(su.M0, su.M1, mpu);
+    if constexpr (GATE) mins_pairs(sg.M0, sg.M1, mpg);
 #pragma unroll
     for (int b = 0; b < MMQ_MAX_BLOCKS; ++b) {
         if (b >= nb) break;
@@ -313,9 +321,8 @@ __device__ __forceinline__ void mmq_superblock(const uint8_t *wrow_up, const uin
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const v4u s4 = *(const v4u *) (rec + MMQ_REC_SUM + 16 * (4 * kq + i));
-            acc[b][i] += mmq_superblock_value(d8a[i], su.d, su.dmin, iu[i], mins_dot(su.M0, su.M1, s4));
-            if constexpr (GATE)
-                accg[b][i] += mmq_superblock_value(d8a[i], sg.d, sg.dmin, ig[i], mins_dot(sg.M0, sg.M1, s4));
+            acc[b][i] += mmq_superblock_value(d8a[i], su.d, su.dmin, iu[i], mins_dot(mpu, s4));
+            if constexpr (GATE) accg[b][i] += mmq_superblock_value(d8a[i], sg.d, sg.dmin, ig[i], mins_dot(mpg, s4));
         }
     }
 }
