@@ -759,7 +759,7 @@ __device__ __forceinline__ void quantize_row_lds(const float *x, uint8_t *q, int
         float amax = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
-        amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
+        amax = fmaxf(amax, xor_lanes<1>(amax));              // the partner lane of the block
         const float d = amax / 127.0f;
         u32 packed[4];
 #pragma unroll
@@ -861,10 +861,9 @@ __device__ __forceinline__ float max8(float v) {
 // code = amax == 0 ? 0 : roundf(v / d), and the block sum in the quantizer's
 // xor-butterfly order (offsets 16, 8, 4 across lanes, then 2, 1 inside the lane).
 // WITH_SUM = false leaves the sum field 0: the K-quant dots read only d and the codes.
-// S16: also the 16-value code sums of the chunk into s16[16 j ..].
-template <bool WITH_SUM = true, bool S16 = false>
+template <bool WITH_SUM = true>
 __device__ __forceinline__ void quantize_chunk(const float xv[4], bool norm, float s, const v4f nwv, uint8_t *y,
-                                               int j, int16_t *s16 = nullptr) {
+                                               int j) {
     const int lane = threadIdx.x % WAVE;
     float v[4] = {xv[0], xv[1], xv[2], xv[3]};
     if (norm) {
@@ -904,13 +903,6 @@ __device__ __forceinline__ void quantize_chunk(const float xv[4], bool norm, flo
     *(u32 *) (yb + 4 + (i % 32)) = packed;
     // the eight lanes of a block store the same scale word (no branch around the store)
     *(u32 *) yb = (u32) f2h_bits(d) | (WITH_SUM ? ((u32) f2h_bits(sum) << 16) : 0u);
-    if constexpr (S16) {
-        // sums of each 16 codes of the chunk (lanes 4m .. 4m+3 hold sub-block m): quad sums by DPP
-        int cs = sdot4(packed, 0x01010101u, 0);
-        cs += __builtin_amdgcn_update_dpp(0, cs, 0xB1, 0xF, 0xF, false);
-        cs += __builtin_amdgcn_update_dpp(0, cs, 0x4E, 0xF, 0xF, false);
-        s16[16 * j + lane / 4] = (int16_t) cs;    // the four lanes of a quad store the same value
-    }
 }
 
 // 16-value sums of the codes of a q8_1 row of k values in LDS (36-byte blocks from p,
@@ -933,7 +925,8 @@ __device__ __forceinline__ void row_sums16_lds(const uint8_t *p, int k, int16_t 
 // The same arithmetic for N chunks of one wave, written stage by stage so that the N
 // dependency chains (cross-lane steps, divisions) interleave instead of running one
 // after another.  rms_chunk_sums = rms_chunk_sum per chunk; quantize_chunks =
-// quantize_chunk<false, true> per chunk under norm (chunk index j[i]).
+// quantize_chunk<false> per chunk under norm (chunk index j[i]), plus the 16-value code
+// sums of each chunk into s16[16 j[i] ..].
 template <int N>
 __device__ __forceinline__ void rms_chunk_sums(const v4f xv[N], float out[N]) {
     float a[N];
