@@ -258,10 +258,11 @@ __global__ __launch_bounds__(FFN_DN_MAX_WAVES *WAVE) void mc_ffn_down_combine_ke
     } else {
         step_issue<TW>(a, s, span);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     float v = 0.0f;                                     // an out-of-range expert id contributes 0
     int nu = 1;
     if (s.valid) {
+        // the activation row went out first: it is in LDS while the weights still land
+        wait_loads_at_most(s.n_up);
         const uint8_t *arow = span + a.lds_act + alead;
         if constexpr (ACT == ACT_F32) {
             quantize_row_lds((const float *) arow, span + a.lds_q8, a.ncols);
@@ -271,6 +272,7 @@ __global__ __launch_bounds__(FFN_DN_MAX_WAVES *WAVE) void mc_ffn_down_combine_ke
         static_assert(AQ == ACT_Q8_1, "down + combine reads q8_1 rows");
         int16_t *rs16 = (int16_t *) (span + a.lds_sums);
         row_sums16_lds(arow, a.ncols, rs16);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         float su = 0.0f, sg = 0.0f;
         if (sh) {
             if constexpr (TS != 0) {
@@ -285,6 +287,7 @@ __global__ __launch_bounds__(FFN_DN_MAX_WAVES *WAVE) void mc_ffn_down_combine_ke
             v = routed_value(a, s, s.row0 + (rl < s.nrows_here ? rl : 0), su, sg);
         }
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");     // an invalid step's activation DMA too
     {
         const int rl = lane / nu;
         if (s.valid) {

@@ -58,8 +58,8 @@ __device__ __forceinline__ void run_step(const GemvArgs &a, uint8_t *lds, bool s
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         return;
     }
-    // activation and gate span landed (the gate dot then runs while the up span lands)
-    wait_loads_at_most(s.wgate ? s.n_up : 0);
+    // the activation row went out first: it is in LDS while the weight spans still land
+    wait_loads_at_most(s.n_gate + s.n_up);
     const uint8_t *arow = lds + a.lds_act + alead;
     if constexpr (ACT == ACT_F32) {
         // fp32 activations: the wave quantizes its staged row to q8_1 blocks in LDS
@@ -71,8 +71,10 @@ __device__ __forceinline__ void run_step(const GemvArgs &a, uint8_t *lds, bool s
         // the row's 16-value code sums, once per wave (min / offset terms of the dots)
         int16_t *rs16 = (int16_t *) (lds + a.lds_sums);
         row_sums16_lds(arow, a.ncols, rs16);
+        wait_loads_at_most(s.wgate ? s.n_up : 0);       // gate span landed (its dot runs while up lands)
         step_dots<T, AQ, true>(a, s, lds, arow, su, sg, rs16);
     } else {
+        wait_loads_at_most(s.wgate ? s.n_up : 0);
         step_dots<T, AQ>(a, s, lds, arow, su, sg);
     }
     step_store<T>(a, s, su, sg);
