@@ -41,6 +41,9 @@ def _norm_q8_1(torch, mc, x, nw, eps):
     ("Q3_K", None, 1024, 128, 1, True, False),
     ("Q6_K", "Q5_K", 1024, 64, 2, True, True),
     ("Q5_K", "Q2_K", 768, 200, 1, True, False),
+    # rows longer than 16 chunks: eight chunks per prologue wave
+    ("Q2_K", "Q4_K", 6144, 96, 2, True, True),
+    ("Q4_K", "Q2_K", 8192, 64, 1, False, False),
 ])
 def test_gate_up_norm_equals_norm_then_gemv(torch_gpu, mc, wtype, sh_type, K, R, n_tok, with_nw, bad_id):
     torch = torch_gpu
