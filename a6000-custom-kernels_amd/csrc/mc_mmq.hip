@@ -6,9 +6,11 @@
 // ggml (MMQ; results/final.patch:45-48 only routes batch-1 decode to the
 // pointer-table GEMV).  Activations are q8_K rows (one scale per 256 values,
 // exact 16-value sums), the ggml-CPU vec_dot_type of the K-quants
-// (patches/trace-hook/ggml-cpu.c:308-340): the eight 32-value sub-block
-// products of a super-block then accumulate exactly in int32 (sub-block scale
-// times the MFMA result), with one float update per super-block.
+// (patches/trace-hook/ggml-cpu.c:308-340): the sub-block products of a
+// super-block then accumulate exactly in int32, with one float update per
+// super-block.  Q4_K/Q5_K scale each 32-value MFMA result by its 6-bit
+// sub-block scale; Q2_K (16-value groups) folds its 4-bit scales into the
+// weight codes and takes the min term from a second MFMA.
 //
 // Three launches:
 //   1. mc_mmq_group_kernel  (one workgroup): pair counts per expert, offsets,
@@ -183,21 +185,29 @@ __global__ __launch_bounds__(256) void mc_mmq_pack_kernel(const MmqArgs a) {
 // 3. grouped GEMM
 // ---------------------------------------------------------------------------
 
-// Issues the DMA of super-block s: MMQ_ROWS weight rows (one 144-byte Q4_K/176-byte
-// Q5_K super-block each, rows row_bytes apart) and nb activation records.
+// Bytes per lane of the weight-tile DMA: 16 where a super-block is a whole number of
+// 16-byte chunks (Q4_K 144, Q5_K 176), else 4 (Q2_K 84: 21 dwords).
+template <int T>
+constexpr int mmq_dma_bytes() { return type_geom(T).block_bytes % 16 == 0 ? 16 : 4; }
+
+// Issues the DMA of super-block s: MMQ_ROWS weight rows (one super-block each,
+// rows row_bytes apart, landing back to back in LDS) and nb activation records.
 template <int T>
 __device__ __forceinline__ void mmq_issue(const MmqArgs &a, const uint8_t *wbase, int row0, int s, int blk0, int nb,
                                           uint8_t *wl, uint8_t *rl) {
     constexpr int SBB = type_geom(T).block_bytes;           // bytes of one super-block
-    constexpr int CH = SBB / 16;                            // 16-byte chunks per super-block
+    constexpr int DB = mmq_dma_bytes<T>();
+    constexpr int CH = SBB / DB;                            // DMA chunks per super-block
     const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
     const uint32_t row_bytes = (uint32_t) (a.ncols / 256) * SBB;
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(wbase, (uint32_t) a.expert_bytes);
     for (int i = wave; i < CH * MMQ_ROWS / WAVE; i += MMQ_WAVES) {
         const int q = i * WAVE + lane;                       // chunk q of the tile: row q / CH, part q % CH
-        const uint32_t off = (uint32_t) (row0 + q / CH) * row_bytes + (uint32_t) s * SBB + 16u * (uint32_t) (q % CH);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void_t *) (wl + 1024 * i), 16, off, 0, 0, 0);
+        const uint32_t off = (uint32_t) (row0 + q / CH) * row_bytes + (uint32_t) s * SBB + (uint32_t) DB * (uint32_t) (q % CH);
+        if constexpr (DB == 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void_t *) (wl + WAVE * DB * i), 16, off, 0, 0, 0);
+        else __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void_t *) (wl + WAVE * DB * i), 4, off, 0, 0, 0);
     }
+    if (nb <= 0) return;
     const uint8_t *recs = a.ws + a.ws_packed + ((int64_t) s * a.max_blocks + blk0) * MMQ_REC_BYTES;
     const __amdgpu_buffer_rsrc_t rr = make_rsrc(recs, (uint32_t) nb * MMQ_REC_BYTES);
     const int rounds = (nb * MMQ_REC_BYTES + 1023) / 1024;
@@ -327,11 +337,84 @@ __device__ __forceinline__ void mmq_superblock(const uint8_t *wrow_up, const uin
     }
 }
 
+// B fragments of one Q2_K row super-block (84 bytes at w: scales[16], qs[64], d, dmin)
+// for this lane (weight row lane % 16, values 8 kq .. 8 kq + 7 of each 32-value
+// sub-block, kq = lane / 16).  Element 128 h + 32 j + l is bits 2j of qs[32 h + l]
+// in 16-value group 8 h + 2 j + l / 16; a lane's eight values share one group.
+//   bq[sb]: the codes times the group's 4-bit scale (at most 3 * 15 = 45, so one
+//           32-bit multiply scales four bytes without carries);
+//   bm[sb]: the group's 4-bit min in all eight bytes (its MFMA against the
+//           activation codes is the min term's sum over the group).
+__device__ __forceinline__ void q2K_frags(const u32 *w, int kq, long (&bq)[8], long (&bm)[8]) {
+    const int hk = kq >> 1;                                 // which half of the 32 values
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const u32 c0 = w[4 + 8 * h + 2 * kq], c1 = w[4 + 8 * h + 2 * kq + 1];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            // scales[8 h + 2 j + hk] = byte 2 (j & 1) + hk of word 2 h + j / 2
+            const u32 sbyte = (w[2 * h + (j >> 1)] >> (8 * (2 * (j & 1) + hk))) & 0xFFu;
+            const u32 sc = sbyte & 0xFu, m = sbyte >> 4;
+            const u32 lo = ((c0 >> (2 * j)) & 0x03030303u) * sc;
+            const u32 hi = ((c1 >> (2 * j)) & 0x03030303u) * sc;
+            const u32 mm = m * 0x01010101u;
+            bq[4 * h + j] = (long) (((uint64_t) hi << 32) | lo);
+            bm[4 * h + j] = (long) (((uint64_t) mm << 32) | mm);
+        }
+    }
+}
+
+// Q2_K: one super-block of the wave's 16-row tile against nb column blocks.  The
+// scaled-code and min MFMAs accumulate the super-block's isum and msum directly
+// (exact int32), then one float update per pair as for the other K-quants.
+template <bool GATE>
+__device__ __forceinline__ void mmq_superblock_q2K(const uint8_t *wrow_up, const uint8_t *wrow_gate,
+                                                   const uint8_t *recs, int nb, float (&acc)[MMQ_MAX_BLOCKS][4],
+                                                   float (&accg)[MMQ_MAX_BLOCKS][4]) {
+    const int lane = threadIdx.x % WAVE;
+    const int kq = lane / 16;
+    const u32 *wu = (const u32 *) wrow_up;
+    const u32 *wg = (const u32 *) wrow_gate;
+    long qu[8], mu[8], qg[8], mg[8];
+    q2K_frags(wu, kq, qu, mu);
+    const float du = h2f(wu[20]), dmu = h2f(wu[20] >> 16);
+    float dg = 0.0f, dmg = 0.0f;
+    if constexpr (GATE) {
+        q2K_frags(wg, kq, qg, mg);
+        dg = h2f(wg[20]);
+        dmg = h2f(wg[20] >> 16);
+    }
+#pragma unroll
+    for (int b = 0; b < MMQ_MAX_BLOCKS; ++b) {
+        if (b >= nb) break;
+        const uint8_t *rec = recs + b * MMQ_REC_BYTES;
+        const long *af = (const long *) (rec + MMQ_REC_FRAG);
+        v4i iu = {0, 0, 0, 0}, su = {0, 0, 0, 0}, ig = {0, 0, 0, 0}, sg = {0, 0, 0, 0};
+#pragma unroll
+        for (int sb = 0; sb < 8; ++sb) {
+            const long a = af[sb * 64 + lane];
+            iu = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, qu[sb], iu, 0, 0, 0);
+            su = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, mu[sb], su, 0, 0, 0);
+            if constexpr (GATE) {
+                ig = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, qg[sb], ig, 0, 0, 0);
+                sg = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, mg[sb], sg, 0, 0, 0);
+            }
+        }
+        const v4f d8 = *(const v4f *) (rec + MMQ_REC_D8 + 16 * kq);
+        const float d8a[4] = {d8.x, d8.y, d8.z, d8.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc[b][i] += mmq_superblock_value(d8a[i], du, dmu, iu[i], su[i]);
+            if constexpr (GATE) accg[b][i] += mmq_superblock_value(d8a[i], dg, dmg, ig[i], sg[i]);
+        }
+    }
+}
+
 template <int T, bool GATE>
 __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const MmqArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int SBB = type_geom(T).block_bytes;
-    constexpr int CH = SBB / 16;
+    constexpr int CH = SBB / mmq_dma_bytes<T>();
     constexpr uint32_t WT = MMQ_ROWS * SBB;                 // weight tile bytes per matrix and super-block
     const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
     const int e = blockIdx.y;
@@ -372,7 +455,8 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
             const uint8_t *st = lds + (uint32_t) (s & 1) * stage;
             const uint8_t *recs = st + (GATE ? 2 : 1) * WT;
             const uint32_t roff = (uint32_t) (16 * wave + lane % 16) * SBB;
-            mmq_superblock<T, GATE>(st + roff, st + WT + roff, recs, nb, acc, accg);
+            if constexpr (T == T_Q2_K) mmq_superblock_q2K<GATE>(st + roff, st + WT + roff, recs, nb, acc, accg);
+            else mmq_superblock<T, GATE>(st + roff, st + WT + roff, recs, nb, acc, accg);
             lds_barrier();                                    // stage s is free for s + 2
         }
         // scatter: pair 4 (lane / 16) + i of each block, weight row lane % 16 of the wave's tile
@@ -430,6 +514,7 @@ int launch_mmq(const MmqArgs &a, int type, void *stream) {
     hipLaunchKernelGGL(mc_mmq_pack_kernel, dim3((unsigned) ((threads + 255) / 256)), dim3(256), 0, s, a);
     if ((err = hipGetLastError()) != hipSuccess) return (int) err;
     switch (type) {
+        case T_Q2_K: return (int) launch_mmq_t<T_Q2_K>(a, s);
         case T_Q4_K: return (int) launch_mmq_t<T_Q4_K>(a, s);
         case T_Q5_K: return (int) launch_mmq_t<T_Q5_K>(a, s);
         default: return (int) hipErrorInvalidValue;

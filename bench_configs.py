@@ -10,7 +10,7 @@
          seeded routings per point;
   cfg5a  the prefill-shaped FFN: 512 tokens x top-8 over 512 Q4_K experts through
          the expert-grouped int8-MFMA path (q8_K of x, gate/up + SwiGLU, q8_K of
-         the GLU rows, down);
+         the GLU rows, down); cfg5a_q2K is the same shape over Q2_K experts;
   cfg3   the pointer-table cache under mixed residency: 40 layers of Q2_K experts
          (63 GB) in pinned host memory, an HBM pool holding 435 of 512 experts per
          tensor, Zipf(1.1) routing, 256 decode tokens with the miss log and LRU
@@ -21,7 +21,7 @@ stream, so host launch cost is excluded.  Bytes are algorithmic: the unique
 expert matrices a launch touches plus activations and outputs.  cpu_baseline
 (cfg1) is the CPU oracle's ggml-CPU MUL_MAT_ID restatement on this host.
 
-Usage: python bench_configs.py [--configs cfg1,cfg3,cfg4,cfg5a] [--rounds N]
+Usage: python bench_configs.py [--configs cfg1,cfg3,cfg4,cfg5a,cfg5a_q2K] [--rounds N]
 """
 from __future__ import annotations
 
@@ -149,13 +149,13 @@ def cfg4(torch, mc, md, rounds):
         torch.cuda.empty_cache()
 
 
-def cfg5a(torch, mc, md, rounds):
+def prefill_ffn(torch, mc, md, rounds, wtype, name):
     E, H, F, U, T = 512, 4096, 768, 8, 512
     gen = torch.Generator(device="cuda")
     gen.manual_seed(31)
-    gate = md.random_expert_tensor(torch, mc.Q4_K, E, F, H, gen)
-    up = md.random_expert_tensor(torch, mc.Q4_K, E, F, H, gen)
-    down = md.random_expert_tensor(torch, mc.Q4_K, E, H, F, gen)
+    gate = md.random_expert_tensor(torch, wtype, E, F, H, gen)
+    up = md.random_expert_tensor(torch, wtype, E, F, H, gen)
+    down = md.random_expert_tensor(torch, wtype, E, H, F, gen)
     ids_np, _ = md.make_routing(T, 1, E, U, seed=32)
     ids = torch.from_numpy(ids_np.reshape(T, U)).cuda()
     x = torch.randn((T, H), generator=gen, device="cuda")
@@ -172,32 +172,42 @@ def cfg5a(torch, mc, md, rounds):
         mc.check(mc.lib().ggml_hip_quantize_q8_K(x.data_ptr(), yx.data_ptr(), H, T, H, H // 256, s()), "q8_K x")
 
     def gu():
-        mc.mul_mat_q(wtype=mc.Q4_K, weights=up, gate=gate, ids=ids, y=yx, dst=h, K=H, R=F, n_experts=E, workspace=ws)
+        mc.mul_mat_q(wtype=wtype, weights=up, gate=gate, ids=ids, y=yx, dst=h, K=H, R=F, n_experts=E, workspace=ws)
 
     def q_h():
         mc.check(mc.lib().ggml_hip_quantize_q8_K(h.data_ptr(), yh.data_ptr(), F, T * U, F, F // 256, s()),
                  "q8_K h")
 
     def dn():
-        mc.mul_mat_q(wtype=mc.Q4_K, weights=down, ids=ids, y=yh, dst=o, K=F, R=H, n_experts=E, nchannels_y=U,
+        mc.mul_mat_q(wtype=wtype, weights=down, ids=ids, y=yh, dst=o, K=F, R=H, n_experts=E, nchannels_y=U,
                      workspace=ws)
 
     ms_all = graph_ms(torch, [q_x, gu, q_h, dn], rounds)
     ms_gu = graph_ms(torch, [gu], rounds)
     ms_dn = graph_ms(torch, [dn], rounds)
-    eb = mc.row_bytes(mc.Q4_K, H) * F
+    eb = mc.row_bytes(wtype, H) * F
     touched = len(set(ids_np.reshape(-1).tolist()))
     wbytes = touched * 3 * eb
     ops = 2 * T * U * 3 * F * H
     gbs = wbytes / (ms_all * 1e-3) / 1e9
-    emit({"config": "cfg5a", "workload": "prefill FFN, 512 tokens x top-8 of 512 Q4_K experts (hidden 4096, ffn 768), "
-                                         "q8_K activations, int8 MFMA grouped GEMM",
+    tname = {mc.Q2_K: "Q2_K", mc.Q4_K: "Q4_K"}[wtype]
+    emit({"config": name, "workload": f"prefill FFN, 512 tokens x top-8 of 512 {tname} experts (hidden 4096, "
+                                      "ffn 768), q8_K activations, int8 MFMA grouped GEMM",
           "us_per_layer": round(ms_all * 1000, 1), "us_gate_up": round(ms_gu * 1000, 1),
           "us_down": round(ms_dn * 1000, 1), "experts_touched": touched, "weight_bytes": wbytes,
           "GB/s": round(gbs, 1), "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
           "int8_ops": ops, "TOP/s": round(ops / (ms_all * 1e-3) / 1e12, 2),
           "mfma_frac": round(ops / (ms_all * 1e-3) / PEAK_INT8_OPS, 4),
           "tok_per_s": round(T / (ms_all * 1e-3), 1)})
+
+
+def cfg5a(torch, mc, md, rounds):
+    prefill_ffn(torch, mc, md, rounds, mc.Q4_K, "cfg5a")
+
+
+def cfg5a_q2K(torch, mc, md, rounds):
+    """The same prefill shape over Q2_K experts (the decode model's routed type)."""
+    prefill_ffn(torch, mc, md, rounds, mc.Q2_K, "cfg5a_q2K")
 
 
 def _hip_runtime(torch):
@@ -346,7 +356,7 @@ def cfg3(torch, mc, md, rounds, tokens=256, calib_tokens=32, layers=40):
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--configs", default="cfg1,cfg4,cfg5a")
+    ap.add_argument("--configs", default="cfg1,cfg4,cfg5a,cfg5a_q2K")
     ap.add_argument("--rounds", type=int, default=10)
     args = ap.parse_args()
     import torch
@@ -355,7 +365,7 @@ def main():
     assert torch.cuda.is_available(), "bench_configs.py needs a HIP device"
     for name in args.configs.split(","):
         log(f"running {name}")
-        {"cfg1": cfg1, "cfg3": cfg3, "cfg4": cfg4, "cfg5a": cfg5a}[name](torch, mc, md, args.rounds)
+        {"cfg1": cfg1, "cfg3": cfg3, "cfg4": cfg4, "cfg5a": cfg5a, "cfg5a_q2K": cfg5a_q2K}[name](torch, mc, md, args.rounds)
 
 
 if __name__ == "__main__":

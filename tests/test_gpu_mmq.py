@@ -28,7 +28,7 @@ def _q8_K_rows(torch, mc, x):
     return buf
 
 
-@pytest.mark.parametrize("wtype", [12, 13])
+@pytest.mark.parametrize("wtype", [10, 12, 13])
 @pytest.mark.parametrize("E,K,R,n_tok,n_used", [(16, 512, 100, 40, 4), (64, 4096, 256, 96, 8)])
 def test_mul_mat_q_matches_ggml_cpu(torch_gpu, mc, O, wtype, E, K, R, n_tok, n_used):
     torch = torch_gpu
@@ -59,10 +59,11 @@ def test_mul_mat_q_matches_ggml_cpu(torch_gpu, mc, O, wtype, E, K, R, n_tok, n_u
     assert np.all(got[~valid] == sentinel)
 
 
-def test_mul_mat_q_gate_glu(torch_gpu, mc, O):
+@pytest.mark.parametrize("wtype,R", [(12, 136), (10, 100)])
+def test_mul_mat_q_gate_glu(torch_gpu, mc, O, wtype, R):
     torch = torch_gpu
-    wtype, E, K, R, n_tok, n_used = 12, 24, 1024, 136, 48, 6
-    _note("mul_mat_q gate+GLU")
+    E, K, n_tok, n_used = 24, 1024, 48, 6
+    _note(f"mul_mat_q gate+GLU type={wtype} R={R}")
     up = H.weights(wtype, E, R, K, seed=1201)
     gate = H.weights(wtype, E, R, K, seed=1202)
     x = H.activations(n_tok, K, seed=1203)
