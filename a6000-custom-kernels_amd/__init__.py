@@ -112,6 +112,8 @@ SIGNATURES = [
     ("ggml_hip_moe_cache_stamps_snapshot", C.c_int, [_I32, _VP, _I32, _VP]),
     ("ggml_hip_moe_cache_totals", C.c_int, [C.POINTER(Totals)]),
     ("ggml_hip_moe_cache_reset", C.c_int, []),
+    ("ggml_hip_moe_trace_append", C.c_int, [C.c_char_p, C.c_char_p, C.c_void_p, _I64, _I64, _I64]),
+    ("ggml_hip_moe_trace_close", C.c_int, []),
     ("ggml_hip_moe_last_error", C.c_char_p, []),
     ("ggml_hip_moe_version", C.c_char_p, []),
 ]

@@ -683,6 +683,10 @@ int quantize_common(int kind, const float *x, void *y, int64_t k, int64_t nrows,
     return 0;
 }
 
+// routing trace files opened by ggml_hip_moe_trace_append: path -> append stream
+std::mutex g_trace_mutex;
+std::unordered_map<std::string, FILE *> g_trace_files;
+
 }  // namespace
 }  // namespace mc
 
@@ -1136,6 +1140,44 @@ int ggml_hip_moe_cache_reset(void) {
     }
     if (first_rc) return dev_err(first_rc, "reset free");
     return 0;
+}
+
+// ---------------------------------------------------------------------------
+// routing trace (patches/trace-hook/ggml-cpu.c:1597-1617)
+// ---------------------------------------------------------------------------
+
+int ggml_hip_moe_trace_append(const char *path, const char *name, const int32_t *ids, int64_t n_used, int64_t n_tok,
+                              int64_t n_exp) {
+    if (!path) path = env2("GGML_HIP_MOE_TRACE", "GGML_MOE_TRACE");
+    if (!path || !*path) return 0;
+    if (n_used < 0 || n_tok < 0 || n_exp < 0 || n_used > 0xFFFFFFFFll || n_tok > 0xFFFFFFFFll ||
+        n_exp > 0xFFFFFFFFll || (n_used * n_tok > 0 && !ids))
+        return fail(E_INVALID, "trace_append: bad record (n_used %lld, n_tok %lld, n_exp %lld)", (long long) n_used,
+                    (long long) n_tok, (long long) n_exp);
+    // the hook copies the name into a zeroed 128-byte buffer with strncpy(.., 120)
+    char nbuf[128] = {0};
+    strncpy(nbuf, name ? name : "?", 120);
+    const uint32_t hdr[4] = {(uint32_t) strlen(nbuf), (uint32_t) n_used, (uint32_t) n_tok, (uint32_t) n_exp};
+    std::lock_guard<std::mutex> lock(g_trace_mutex);
+    FILE *&f = g_trace_files[path];
+    if (!f && !(f = fopen(path, "ab"))) {
+        g_trace_files.erase(path);
+        return fail(E_INVALID, "trace_append: cannot open %s: %s", path, strerror(errno));
+    }
+    const size_t n_ids = (size_t) (n_used * n_tok);
+    if (fwrite(hdr, sizeof(uint32_t), 4, f) != 4 || fwrite(nbuf, 1, hdr[0], f) != hdr[0] ||
+        (n_ids && fwrite(ids, sizeof(int32_t), n_ids, f) != n_ids))
+        return fail(E_INVALID, "trace_append: write to %s failed", path);
+    return 0;
+}
+
+int ggml_hip_moe_trace_close(void) {
+    std::lock_guard<std::mutex> lock(g_trace_mutex);
+    int rc = 0;
+    for (auto &kv : g_trace_files)
+        if (kv.second && fclose(kv.second) != 0 && !rc) rc = fail(E_INVALID, "trace_close: %s", kv.first.c_str());
+    g_trace_files.clear();
+    return rc;
 }
 
 const char *ggml_hip_moe_last_error(void) { return t_last_error.c_str(); }

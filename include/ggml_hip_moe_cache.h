@@ -350,6 +350,26 @@ int ggml_hip_moe_cache_totals(ggml_hip_moe_totals *out);
  * (the reference has no teardown). */
 int ggml_hip_moe_cache_reset(void);
 
+/* ---------------------------------------------------------------------
+ * Routing trace (patches/trace-hook/ggml-cpu.c:1-9, :1597-1617): one binary
+ * record per MUL_MAT_ID, appended to a file, input of the seed builder
+ * (a6000-custom-kernels_amd/seed.py, the restatement of tools/make_seed.py):
+ *   u32 namelen, u32 n_used, u32 n_tok, u32 n_exp (little endian),
+ *   char name[namelen] (the tensor name cut to 120 bytes, no terminator),
+ *   i32 ids[n_used * n_tok] (token-major, ggml's ids layout).
+ * ---------------------------------------------------------------------
+ *
+ * Appends one record to `path` (NULL: the file named by GGML_HIP_MOE_TRACE,
+ * alias GGML_MOE_TRACE; no such variable: nothing is written and 0 is returned).
+ * ids is host memory.  The file is opened in append mode on first use and kept
+ * open, as the reference's hook does; records from concurrent callers are
+ * serialised.  Returns 0 or a negative status (open/write failure, bad sizes). */
+int ggml_hip_moe_trace_append(const char *path, const char *name, const int32_t *ids,
+                              int64_t n_used, int64_t n_tok, int64_t n_exp);
+
+/* Flushes and closes every trace file opened by ggml_hip_moe_trace_append. */
+int ggml_hip_moe_trace_close(void);
+
 /* Text of the last error on this thread. */
 const char *ggml_hip_moe_last_error(void);
 
