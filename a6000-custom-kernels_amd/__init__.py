@@ -112,6 +112,9 @@ SIGNATURES = [
     ("ggml_hip_moe_cache_stamps_snapshot", C.c_int, [_I32, _VP, _I32, _VP]),
     ("ggml_hip_moe_cache_totals", C.c_int, [C.POINTER(Totals)]),
     ("ggml_hip_moe_cache_reset", C.c_int, []),
+    ("ggml_hip_ssm_conv_f32", C.c_int,
+     [_VP, _I64, _I64, _I64, _VP, C.c_int32, _I64, _VP, C.c_int32, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+      _VP]),
     ("ggml_hip_moe_trace_append", C.c_int, [C.c_char_p, C.c_char_p, C.c_void_p, _I64, _I64, _I64]),
     ("ggml_hip_moe_trace_close", C.c_int, []),
     ("ggml_hip_moe_last_error", C.c_char_p, []),
@@ -333,6 +336,33 @@ def mul_mat_q(*, wtype, weights, ids, y, dst, K, R, n_experts, gate=None, glu_op
                                       workspace.numel(), _stream(stream))
     check(rc, "mul_mat_q")
     return dst
+
+
+def ssm_conv(x, w, *, bias=None, silu=False, out=None, n_t=None, stream=None):
+    """SSM_CONV through ggml_hip_ssm_conv_f32.
+
+    x: float32 [n_s, nr, nc - 1 + n_t] (conv_x, rows contiguous); w: float32 or float16 [nr, nc];
+    bias: float32 [nr] (with silu only); out: float32 [n_s, n_t, nr] (allocated when None).
+    """
+    torch = _torch()
+    n_s, nr, cols = x.shape
+    nc = w.shape[1]
+    n_t = cols - nc + 1 if n_t is None else n_t
+    if out is None:
+        out = torch.empty((n_s, n_t, nr), dtype=torch.float32, device=x.device)
+    _require_gpu(x, w, bias, out)
+    if w.dtype == torch.float16:
+        wt = 1
+    elif w.dtype == torch.float32:
+        wt = 0
+    else:
+        raise TypeError("ssm_conv: weights must be float32 or float16")
+    es = w.element_size()
+    rc = lib().ggml_hip_ssm_conv_f32(x.data_ptr(), x.stride(2) * 4, x.stride(1) * 4, x.stride(0) * 4, w.data_ptr(), wt,
+                                     w.stride(0) * es, _ptr(bias), 1 if silu else 0, out.data_ptr(), out.stride(2) * 4,
+                                     out.stride(1) * 4, out.stride(0) * 4, nc, nr, n_t, n_s, _stream(stream))
+    check(rc, "ssm_conv")
+    return out
 
 
 def configure(*, enabled=True, slots=-1, budget_gb=0.0, margin_gb=2.0, seed_path=None, max_promotions=48,

@@ -38,6 +38,7 @@ SOURCES = [
     ("mc_kernels.hip", "hip"),
     ("mc_mmq.hip", "hip"),
     ("mc_ffn.hip", "hip"),
+    ("mc_ssm_conv.hip", "hip"),
     ("mc_device_hip.cpp", "hiphost"),
     ("mc_host.cpp", "cxx"),
 ]

@@ -35,6 +35,7 @@ struct Device {
     virtual int launch_quantize(int kind, const QuantArgs &q, void *stream) = 0;
     virtual int launch_combine(const CombineArgs &c, void *stream) = 0;
     virtual int launch_mmq(const MmqArgs &m, int type, void *stream) = 0;
+    virtual int launch_ssm_conv(const SsmConvArgs &a, void *stream) = 0;
     virtual const char *error_string(int code) = 0;
 };
 

@@ -9,6 +9,7 @@ int launch_gemv(GemvArgs a, int tw, int ts, int act, void *stream);   // mc_kern
 int launch_quantize(int kind, const QuantArgs &q, void *stream);      // mc_kernels.hip
 int launch_combine(const CombineArgs &c, void *stream);               // mc_kernels.hip
 int launch_mmq(const MmqArgs &m, int type, void *stream);            // mc_mmq.hip
+int launch_ssm_conv(const SsmConvArgs &a, void *stream);              // mc_ssm_conv.hip
 
 namespace {
 
@@ -54,6 +55,7 @@ struct HipDevice final : Device {
     int launch_quantize(int kind, const QuantArgs &q, void *s) override { return mc::launch_quantize(kind, q, s); }
     int launch_combine(const CombineArgs &c, void *s) override { return mc::launch_combine(c, s); }
     int launch_mmq(const MmqArgs &m, int type, void *s) override { return mc::launch_mmq(m, type, s); }
+    int launch_ssm_conv(const SsmConvArgs &a, void *s) override { return mc::launch_ssm_conv(a, s); }
     const char *error_string(int code) override { return hipGetErrorString((hipError_t) code); }
 };
 

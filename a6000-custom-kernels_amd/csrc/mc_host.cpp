@@ -969,6 +969,49 @@ int ggml_hip_moe_mul_mat_q(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_f
     return 0;
 }
 
+int ggml_hip_ssm_conv_f32(const float *src0, int64_t src0_nb0, int64_t src0_nb1, int64_t src0_nb2, const void *src1,
+                          int32_t src1_type, int64_t src1_nb1, const float *bias, int32_t fuse_silu, float *dst,
+                          int64_t dst_nb0, int64_t dst_nb1, int64_t dst_nb2, int64_t nc, int64_t nr, int64_t n_t,
+                          int64_t n_s, void *stream) {
+    if (!src0 || !src1 || !dst) return fail(E_INVALID, "ssm_conv: null argument");
+    if (src1_type != 0 && src1_type != 1) return fail(E_UNSUPPORTED, "ssm_conv: weight type %d (F32 or F16 only)", src1_type);
+    if (nc != 3 && nc != 4 && nc != 5 && nc != 9 && nc != 15)
+        return fail(E_UNSUPPORTED, "ssm_conv: only kernel sizes 3, 4, 5, 9, 15 are supported (got %lld)", (long long) nc);
+    if (bias && !fuse_silu) return fail(E_INVALID, "ssm_conv: a fused bias comes with the fused SiLU");
+    if (nr <= 0 || n_t < 0 || n_s < 0 || nr > INT32_MAX || n_t > INT32_MAX || n_s > 65535)
+        return fail(E_INVALID, "ssm_conv: bad shape (nr %lld, n_t %lld, n_s %lld)", (long long) nr, (long long) n_t,
+                    (long long) n_s);
+    if (src0_nb0 != 4 || dst_nb0 != 4) return fail(E_INVALID, "ssm_conv: conv_x and dst rows must be contiguous floats");
+    const size_t esz = src1_type ? 2 : 4;
+    if (src0_nb1 < (nc - 1 + n_t) * 4 || (src0_nb1 | src0_nb2) & 3 || (n_s > 1 && src0_nb2 < src0_nb1 * nr))
+        return fail(E_INVALID, "ssm_conv: conv_x strides (nb1 %lld, nb2 %lld)", (long long) src0_nb1, (long long) src0_nb2);
+    if (src1_nb1 < nc * (int64_t) esz || src1_nb1 % (int64_t) esz)
+        return fail(E_INVALID, "ssm_conv: weight row stride %lld", (long long) src1_nb1);
+    if (dst_nb1 < nr * 4 || (dst_nb1 | dst_nb2) & 3 || (n_s > 1 && dst_nb2 < dst_nb1 * n_t))
+        return fail(E_INVALID, "ssm_conv: dst strides (nb1 %lld, nb2 %lld)", (long long) dst_nb1, (long long) dst_nb2);
+    if ((uintptr_t) src0 & 3 || (uintptr_t) dst & 3 || (uintptr_t) src1 & (esz - 1) || (uintptr_t) bias & 3)
+        return fail(E_INVALID, "ssm_conv: misaligned pointer");
+    SsmConvArgs a = {};
+    a.x = src0;
+    a.x_nb1 = src0_nb1;
+    a.x_nb2 = src0_nb2;
+    a.w = src1;
+    a.w_nb1 = src1_nb1;
+    a.w_f16 = src1_type;
+    a.bias = bias;
+    a.silu = fuse_silu ? 1 : 0;
+    a.dst = dst;
+    a.dst_nb1 = dst_nb1;
+    a.dst_nb2 = dst_nb2;
+    a.nc = (int32_t) nc;
+    a.nr = (int32_t) nr;
+    a.n_t = (int32_t) n_t;
+    a.n_s = (int32_t) n_s;
+    const int rc = dev()->launch_ssm_conv(a, stream);
+    if (rc) return dev_err(rc, "ssm_conv launch");
+    return 0;
+}
+
 int ggml_hip_moe_cache_configure(const ggml_hip_moe_config *cfg) {
     if (!cfg) return fail(E_INVALID, "configure: null config");
     std::lock_guard<std::mutex> lock(g_mutex);

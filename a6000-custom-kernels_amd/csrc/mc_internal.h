@@ -198,6 +198,23 @@ struct CombineArgs {
     float eps;
 };
 
+// SSM_CONV (kernels/ssm-conv.cu): dst[s][t][r] = act(sum_j x[s][r][t + j] * w[r][j] (+ bias[r]))
+struct SsmConvArgs {
+    const float *x;          // conv_x: row (s, r) at x + s*x_nb2 + r*x_nb1 bytes, nc - 1 + n_t floats
+    int64_t x_nb1, x_nb2;
+    const void *w;           // taps: row r at w + r*w_nb1 bytes, nc values (F32 or F16)
+    int64_t w_nb1;
+    int32_t w_f16;
+    const float *bias;       // [nr] or null (only with silu)
+    int32_t silu;
+    float *dst;              // element (s, t, r) at dst + s*dst_nb2 + t*dst_nb1 + 4r bytes
+    int64_t dst_nb1, dst_nb2;
+    int32_t nc;              // taps (d_conv)
+    int32_t nr;              // channels (d_inner)
+    int32_t n_t;             // tokens per sequence
+    int32_t n_s;             // sequences
+};
+
 // Canonical order of the RMS sum of a row of k values (k % 256 == 0), shared by
 // the combine kernel and the CPU oracle: chunk j holds values [256j, 256j+256);
 // lane l of a 64-lane group accumulates v = x[256j + 4l + i] for i = 0..3 as

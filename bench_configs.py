@@ -11,6 +11,8 @@
   cfg5a  the prefill-shaped FFN: 512 tokens x top-8 over 512 Q4_K experts through
          the expert-grouped int8-MFMA path (q8_K of x, gate/up + SwiGLU, q8_K of
          the GLU rows, down); cfg5a_q2K is the same shape over Q2_K experts;
+  ssm_conv  SSM_CONV with F16 taps and the fused bias + SiLU (d_conv 4, d_inner
+         8192): 512-token prefill and one-token decode;
   cfg3   the pointer-table cache under mixed residency: 40 layers of Q2_K experts
          (63 GB) in pinned host memory, an HBM pool holding 435 of 512 experts per
          tensor, Zipf(1.1) routing, 256 decode tokens with the miss log and LRU
@@ -19,9 +21,10 @@
 Kernel times come from graph replays timed with HIP events on the replay
 stream, so host launch cost is excluded.  Bytes are algorithmic: the unique
 expert matrices a launch touches plus activations and outputs.  cpu_baseline
-(cfg1) is the CPU oracle's ggml-CPU MUL_MAT_ID restatement on this host.
+(cfg1) is the CPU oracle's ggml-CPU MUL_MAT_ID restatement on this host; the
+ssm_conv line carries the oracle's single-thread SSM_CONV on the same input.
 
-Usage: python bench_configs.py [--configs cfg1,cfg3,cfg4,cfg5a,cfg5a_q2K] [--rounds N]
+Usage: python bench_configs.py [--configs cfg1,cfg3,cfg4,cfg5a,cfg5a_q2K,ssm_conv] [--rounds N]
 """
 from __future__ import annotations
 
@@ -201,6 +204,39 @@ def prefill_ffn(torch, mc, md, rounds, wtype, name):
           "tok_per_s": round(T / (ms_all * 1e-3), 1)})
 
 
+def ssm_conv(torch, mc, md, rounds):
+    """SSM_CONV with F16 taps, fused bias + SiLU (d_conv 4, d_inner 8192): a 512-token
+    prefill over 16 rotating buffer sets (540 MB, past the MALL) and a one-token decode
+    (16 launches per graph replay, time per launch)."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as O
+    nc, nr = 4, 8192
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(41)
+    w = (torch.randn((nr, nc), generator=gen, device="cuda") * 0.5).half()
+    b = torch.randn(nr, generator=gen, device="cuda")
+    for n_t, copies in ((512, 16), (1, 16)):
+        xs = [torch.randn((1, nr, nc - 1 + n_t), generator=gen, device="cuda") for _ in range(copies)]
+        ys = [torch.empty((1, n_t, nr), device="cuda") for _ in range(copies)]
+        launches = [lambda i=i: mc.ssm_conv(xs[i], w, bias=b, silu=True, out=ys[i]) for i in range(copies)]
+        ms = graph_ms(torch, launches, rounds) / copies
+        nbytes = 4 * nr * (nc - 1 + n_t) + 4 * n_t * nr + 2 * nr * nc + 4 * nr
+        line = {"config": f"ssm_conv_t{n_t}",
+                "workload": f"SSM_CONV d_conv {nc}, d_inner {nr}, {n_t} token(s), F16 taps, bias + SiLU",
+                "us_per_call": round(ms * 1000, 2), "bytes": nbytes,
+                "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                "pct_of_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2)}
+        if n_t == 512:
+            x0 = xs[0].cpu().numpy()
+            w0, b0 = w.cpu().numpy(), b.cpu().numpy()
+            t0 = time.perf_counter()
+            O.ssm_conv(x0, w0, bias=b0, silu=True)
+            cpu_s = time.perf_counter() - t0
+            line["cpu_baseline"] = {"us_per_call": round(cpu_s * 1e6, 1), "GB/s": round(nbytes / cpu_s / 1e9, 2),
+                                    "cores": 1, "kind": "port"}
+        emit(line)
+
+
 def cfg5a(torch, mc, md, rounds):
     prefill_ffn(torch, mc, md, rounds, mc.Q4_K, "cfg5a")
 
@@ -356,7 +392,7 @@ def cfg3(torch, mc, md, rounds, tokens=256, calib_tokens=32, layers=40):
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--configs", default="cfg1,cfg4,cfg5a,cfg5a_q2K")
+    ap.add_argument("--configs", default="cfg1,cfg4,cfg5a,cfg5a_q2K,ssm_conv")
     ap.add_argument("--rounds", type=int, default=10)
     args = ap.parse_args()
     import torch
@@ -365,7 +401,8 @@ def main():
     assert torch.cuda.is_available(), "bench_configs.py needs a HIP device"
     for name in args.configs.split(","):
         log(f"running {name}")
-        {"cfg1": cfg1, "cfg3": cfg3, "cfg4": cfg4, "cfg5a": cfg5a, "cfg5a_q2K": cfg5a_q2K}[name](torch, mc, md, args.rounds)
+        {"cfg1": cfg1, "cfg3": cfg3, "cfg4": cfg4, "cfg5a": cfg5a, "cfg5a_q2K": cfg5a_q2K,
+         "ssm_conv": ssm_conv}[name](torch, mc, md, args.rounds)
 
 
 if __name__ == "__main__":

@@ -351,6 +351,26 @@ int ggml_hip_moe_cache_totals(ggml_hip_moe_totals *out);
 int ggml_hip_moe_cache_reset(void);
 
 /* ---------------------------------------------------------------------
+ * SSM_CONV with F32 or F16 conv weights (kernels/ssm-conv.cu:117-217: the
+ * reference's ssm_conv_f32_cuda / ggml_cuda_op_ssm_conv, templated on the
+ * weight type so that F16 conv1d weights work; the fused ADD(bias) + SiLU).
+ *   dst[s][t][r] = act(sum_{j<nc} src0[s][r][t + j] * src1[r][j] (+ bias[r]))
+ * src0 = conv_x (F32, rows of nc - 1 + n_t floats: byte strides src0_nb1 per
+ * channel, src0_nb2 per sequence, src0_nb0 = 4); src1 = conv1d weight, type 0
+ * (F32) or 1 (F16), src1_nb1 bytes per channel; dst F32 with dst_nb0 = 4,
+ * dst_nb1 per token, dst_nb2 per sequence.  fuse_silu applies SiLU; bias (nr
+ * floats) requires it (the reference asserts the same).  nc in {3, 4, 5, 9, 15}
+ * as in the reference; nr need not be a multiple of 128 (the reference asserts
+ * it).  Taps are summed in ascending order with fused multiply-adds from 0,
+ * then the bias is added.
+ * --------------------------------------------------------------------- */
+int ggml_hip_ssm_conv_f32(const float *src0, int64_t src0_nb0, int64_t src0_nb1, int64_t src0_nb2,
+                          const void *src1, int32_t src1_type, int64_t src1_nb1,
+                          const float *bias, int32_t fuse_silu,
+                          float *dst, int64_t dst_nb0, int64_t dst_nb1, int64_t dst_nb2,
+                          int64_t nc, int64_t nr, int64_t n_t, int64_t n_s, void *stream);
+
+/* ---------------------------------------------------------------------
  * Routing trace (patches/trace-hook/ggml-cpu.c:1-9, :1597-1617): one binary
  * record per MUL_MAT_ID, appended to a file, input of the seed builder
  * (a6000-custom-kernels_amd/seed.py, the restatement of tools/make_seed.py):

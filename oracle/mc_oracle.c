@@ -762,6 +762,30 @@ float or_vec_dot(int wt, int act_kind, int64_t k, const void *w, const void *a) 
 
 static float silu(float x) { return x / (1.0f + expf(-x)); }
 
+/* kernels/ssm-conv.cu:5-57: the reference keeps a ring buffer of the last nc inputs,
+ * x[(i + j) % d_conv] = x_block[i + j]; the sum visits the same values in the same order. */
+void or_ssm_conv_f32(const float *x, int64_t x_row, int64_t x_seq, const void *w, int w_f16, int64_t w_row,
+                     const float *bias, int silu_on, float *dst, int64_t dst_tok, int64_t dst_seq,
+                     int64_t nc, int64_t nr, int64_t n_t, int64_t n_s) {
+    for (int64_t s = 0; s < n_s; ++s)
+        for (int64_t r = 0; r < nr; ++r) {
+            const float *xr = x + s * x_seq + r * x_row;
+            float wv[16];
+            for (int64_t j = 0; j < nc && j < 16; ++j)
+                wv[j] = w_f16 ? H2F(((const uint16_t *) w)[r * w_row + j]) : ((const float *) w)[r * w_row + j];
+            const float b = bias ? bias[r] : 0.0f;
+            for (int64_t t = 0; t < n_t; ++t) {
+                float sumf = 0.0f;
+                for (int64_t j = 0; j < nc; ++j) sumf = fmaf(xr[t + j], wv[j], sumf);
+                if (silu_on) {
+                    sumf += b;
+                    sumf = silu(sumf);
+                }
+                dst[s * dst_seq + t * dst_tok + r] = sumf;
+            }
+        }
+}
+
 float or_glu(int op, float g, float up, float limit) {
     switch (op) {
         case OR_GLU_REGLU: return up * (g > 0.0f ? g : 0.0f);

@@ -141,6 +141,16 @@ void or_combine_q8_1(const float *o, int64_t o_stride, const float *w, int32_t n
 /* Sum of squares of k values (k % 256 == 0) in the GPU kernels' fixed order (mc_oracle.c). */
 float or_rms_sum(const float *x, int64_t k);
 
+/* SSM_CONV (kernels/ssm-conv.cu:5-57, ssm_conv_f32): for each sequence s, channel r and
+ * token t, sumf = 0; sumf = fmaf(x[s][r][t + j], w[r][j], sumf) for j = 0..nc-1 (the CUDA
+ * build contracts `sumf += x*w` into fused multiply-adds); with silu: sumf += bias[r] (when
+ * given), then sumf / (1 + expf(-sumf)).  x rows hold nc - 1 + n_t floats (x_row floats
+ * apart, x_seq floats per sequence); w is F32 (w_f16 = 0) or F16 bits, w_row elements per
+ * channel; dst[s][t][r] at s*dst_seq + t*dst_tok + r floats. */
+void or_ssm_conv_f32(const float *x, int64_t x_row, int64_t x_seq, const void *w, int w_f16, int64_t w_row,
+                     const float *bias, int silu, float *dst, int64_t dst_tok, int64_t dst_seq,
+                     int64_t nc, int64_t nr, int64_t n_t, int64_t n_s);
+
 /* Deterministic generator used by the synthetic workloads (splitmix64 + Box-Muller). */
 uint64_t or_splitmix64(uint64_t *state);
 void or_fill_normal(uint64_t seed, float mean, float std, float *out, int64_t n);

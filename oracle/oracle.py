@@ -85,6 +85,8 @@ def lib():
         L.or_combine_q8_1.argtypes = [vp, i64, vp, C.c_int32, vp, i64, vp, vp, vp, i64, i64, C.c_int32, vp, C.c_float]
         L.or_rms_sum.argtypes, L.or_rms_sum.restype = [vp, i64], C.c_float
         L.or_combine_q8_1.restype = None
+        L.or_ssm_conv_f32.argtypes = [vp, i64, i64, vp, C.c_int, i64, vp, C.c_int, vp, i64, i64, i64, i64, i64, i64]
+        L.or_ssm_conv_f32.restype = None
         _lib = L
     return _lib
 
@@ -294,6 +296,22 @@ def combine_q8_1(o, w, shared=None, residual=None, rms_norm=False, norm_weight=N
     lib().or_combine_q8_1(o.ctypes.data, k, w.ctypes.data, n_used, _p(sh), k, _p(res), x.ctypes.data, y.ctypes.data,
                           k, n_tok, int(bool(rms_norm)), _p(nw), eps)
     return x, y
+
+
+def ssm_conv(x, w, bias=None, silu=False):
+    """SSM_CONV: x [n_s, nr, nc - 1 + n_t] float32, w [nr, nc] float32 or float16,
+    bias [nr] (with silu) -> dst [n_s, n_t, nr] float32 (or_ssm_conv_f32)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n_s, nr, cols = x.shape
+    f16 = np.asarray(w).dtype == np.float16
+    w = np.ascontiguousarray(w, dtype=np.float16 if f16 else np.float32)
+    nc = w.shape[1]
+    n_t = cols - nc + 1
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    dst = np.empty((n_s, n_t, nr), np.float32)
+    lib().or_ssm_conv_f32(x.ctypes.data, cols, nr * cols, w.ctypes.data, int(f16), nc, _p(b), int(bool(silu)),
+                          dst.ctypes.data, nr, n_t * nr, nc, nr, n_t, n_s)
+    return dst
 
 
 def rms_sum(x):

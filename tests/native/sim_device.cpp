@@ -126,6 +126,7 @@ struct SimDevice final : Device {
     int launch_quantize(int, const QuantArgs &, void *) override { return 98; }
     int launch_combine(const CombineArgs &, void *) override { return 98; }
     int launch_mmq(const MmqArgs &, int, void *) override { return 98; }
+    int launch_ssm_conv(const SsmConvArgs &, void *) override { return 98; }
     const char *error_string(int code) override {
         return code == 2 ? "out of memory (sim)" : code == 98 ? "not simulated" : "sim error";
     }
