@@ -230,7 +230,12 @@ constexpr int RMS_CHUNK = 256;
 constexpr int MMQ_COLS = 16;              // (token, slot) pairs per column block: the MFMA M dimension
 constexpr int MMQ_WAVES = 4;              // waves per GEMM workgroup, 16 weight rows each
 constexpr int MMQ_ROWS = 16 * MMQ_WAVES;  // weight rows per GEMM workgroup
-constexpr int MMQ_MAX_BLOCKS = 2;         // column blocks multiplied per pass over an expert's weights
+// Column blocks multiplied per pass over an expert's weights: 1 when the experts
+// average at most MMQ_FEW_PAIRS pairs (most need one block, and the smaller LDS
+// stages let more workgroups keep weight DMA in flight), else up to 4 (fewer
+// passes over the weights when experts see many tokens).
+constexpr int MMQ_MAX_BLOCKS = 4;
+constexpr int MMQ_FEW_PAIRS = 12;
 constexpr int MMQ_MAX_EXPERTS = 4096;
 constexpr int MMQ_REC_BYTES = 4416;       // activation record of one (super-block, column block)
 

@@ -20,7 +20,7 @@
 //      32-value sums (zeros for empty columns).
 //   3. mc_mmq_gemm_kernel<T, GATE>: one workgroup per (64 weight rows, expert);
 //      per super-block it DMAs the 64 rows' weight blocks and the records of up
-//      to MMQ_MAX_BLOCKS column blocks into LDS (double-buffered), each wave
+//      to MAXB column blocks into LDS (double-buffered), each wave
 //      multiplies 16 weight rows against them, and the epilogue applies the GLU
 //      (when a gate matrix is fused) and scatters to dst[token][slot][row].
 // The position of a pair inside its expert's group depends on atomic order, but
@@ -295,10 +295,9 @@ __device__ __forceinline__ int mins_dot(const u32 (&mp)[4], const v4u s4) {
 // One super-block of one 16-row weight tile (the wave's rows, the lane's row =
 // lane % 16) of the up matrix (and the gate) against nb column blocks: acc[b][i]
 // for pair 4 (lane / 16) + i of block b.
-template <int T, bool GATE>
+template <int T, bool GATE, int MAXB>
 __device__ __forceinline__ void mmq_superblock(const uint8_t *wrow_up, const uint8_t *wrow_gate, const uint8_t *recs,
-                                               int nb, float (&acc)[MMQ_MAX_BLOCKS][4],
-                                               float (&accg)[MMQ_MAX_BLOCKS][4]) {
+                                               int nb, float (&acc)[MAXB][4], float (&accg)[MAXB][4]) {
     const int lane = threadIdx.x % WAVE;
     const int kq = lane / 16;
     const u32 *wu = (const u32 *) wrow_up;
@@ -310,7 +309,7 @@ __device__ __forceinline__ void mmq_superblock(const uint8_t *wrow_up, const uin
     mins_pairs(su.M0, su.M1, mpu);
     if constexpr (GATE) mins_pairs(sg.M0, sg.M1, mpg);
 #pragma unroll
-    for (int b = 0; b < MMQ_MAX_BLOCKS; ++b) {
+    for (int b = 0; b < MAXB; ++b) {
         if (b >= nb) break;
         const uint8_t *rec = recs + b * MMQ_REC_BYTES;
         const long *af = (const long *) (rec + MMQ_REC_FRAG);
@@ -367,10 +366,10 @@ __device__ __forceinline__ void q2K_frags(const u32 *w, int kq, long (&bq)[8], l
 // Q2_K: one super-block of the wave's 16-row tile against nb column blocks.  The
 // scaled-code and min MFMAs accumulate the super-block's isum and msum directly
 // (exact int32), then one float update per pair as for the other K-quants.
-template <bool GATE>
+template <bool GATE, int MAXB>
 __device__ __forceinline__ void mmq_superblock_q2K(const uint8_t *wrow_up, const uint8_t *wrow_gate,
-                                                   const uint8_t *recs, int nb, float (&acc)[MMQ_MAX_BLOCKS][4],
-                                                   float (&accg)[MMQ_MAX_BLOCKS][4]) {
+                                                   const uint8_t *recs, int nb, float (&acc)[MAXB][4],
+                                                   float (&accg)[MAXB][4]) {
     const int lane = threadIdx.x % WAVE;
     const int kq = lane / 16;
     const u32 *wu = (const u32 *) wrow_up;
@@ -385,7 +384,7 @@ __device__ __forceinline__ void mmq_superblock_q2K(const uint8_t *wrow_up, const
         dmg = h2f(wg[20] >> 16);
     }
 #pragma unroll
-    for (int b = 0; b < MMQ_MAX_BLOCKS; ++b) {
+    for (int b = 0; b < MAXB; ++b) {
         if (b >= nb) break;
         const uint8_t *rec = recs + b * MMQ_REC_BYTES;
         const long *af = (const long *) (rec + MMQ_REC_FRAG);
@@ -410,7 +409,7 @@ __device__ __forceinline__ void mmq_superblock_q2K(const uint8_t *wrow_up, const
     }
 }
 
-template <int T, bool GATE>
+template <int T, bool GATE, int MAXB>
 __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const MmqArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int SBB = type_geom(T).block_bytes;
@@ -426,15 +425,15 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
     const uint8_t *wup = a.w + (int64_t) e * a.expert_bytes;
     const uint8_t *wgt = GATE ? a.w_gate + (int64_t) e * a.expert_bytes : nullptr;
     // LDS: two stages of [up tile | gate tile | records]
-    const uint32_t stage = (GATE ? 2u : 1u) * WT + MMQ_MAX_BLOCKS * MMQ_REC_BYTES + 1024u;
+    const uint32_t stage = (GATE ? 2u : 1u) * WT + MAXB * MMQ_REC_BYTES + 1024u;
     const int *blk_tab = (const int *) (a.ws + a.ws_blk_tab);
     const int *list = (const int *) (a.ws + a.ws_list);
 
-    for (int g0 = 0; g0 < nblk; g0 += MMQ_MAX_BLOCKS) {
-        const int nb = min(MMQ_MAX_BLOCKS, nblk - g0);
-        float acc[MMQ_MAX_BLOCKS][4], accg[MMQ_MAX_BLOCKS][4];
+    for (int g0 = 0; g0 < nblk; g0 += MAXB) {
+        const int nb = min(MAXB, nblk - g0);
+        float acc[MAXB][4], accg[MAXB][4];
 #pragma unroll
-        for (int b = 0; b < MMQ_MAX_BLOCKS; ++b)
+        for (int b = 0; b < MAXB; ++b)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[b][i] = accg[b][i] = 0.0f;
         const int per_stage = mmq_issue_count(nb, wave, CH) + (GATE ? mmq_issue_count(0, wave, CH) : 0);
@@ -455,15 +454,15 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
             const uint8_t *st = lds + (uint32_t) (s & 1) * stage;
             const uint8_t *recs = st + (GATE ? 2 : 1) * WT;
             const uint32_t roff = (uint32_t) (16 * wave + lane % 16) * SBB;
-            if constexpr (T == T_Q2_K) mmq_superblock_q2K<GATE>(st + roff, st + WT + roff, recs, nb, acc, accg);
-            else mmq_superblock<T, GATE>(st + roff, st + WT + roff, recs, nb, acc, accg);
+            if constexpr (T == T_Q2_K) mmq_superblock_q2K<GATE, MAXB>(st + roff, st + WT + roff, recs, nb, acc, accg);
+            else mmq_superblock<T, GATE, MAXB>(st + roff, st + WT + roff, recs, nb, acc, accg);
             lds_barrier();                                    // stage s is free for s + 2
         }
         // scatter: pair 4 (lane / 16) + i of each block, weight row lane % 16 of the wave's tile
         const int row = row0 + 16 * wave + lane % 16;
         if (row < a.nrows) {
 #pragma unroll
-            for (int b = 0; b < MMQ_MAX_BLOCKS; ++b) {
+            for (int b = 0; b < MAXB; ++b) {
                 if (b >= nb) break;
                 const int *tab = blk_tab + 4 * (blk_first + g0 + b);
 #pragma unroll
@@ -484,22 +483,29 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
 // launcher
 // ---------------------------------------------------------------------------
 
-template <int T>
-static hipError_t launch_mmq_t(const MmqArgs &a, hipStream_t s) {
+template <int T, int MAXB>
+static hipError_t launch_mmq_tb(const MmqArgs &a, hipStream_t s) {
     constexpr uint32_t WT = MMQ_ROWS * type_geom(T).block_bytes;
     const bool gate = a.w_gate != nullptr;
-    const uint32_t stage = (gate ? 2u : 1u) * WT + MMQ_MAX_BLOCKS * MMQ_REC_BYTES + 1024u;
+    const uint32_t stage = (gate ? 2u : 1u) * WT + MAXB * MMQ_REC_BYTES + 1024u;
     const dim3 grid((unsigned) ((a.nrows + MMQ_ROWS - 1) / MMQ_ROWS), (unsigned) a.n_experts);
     // more than the default 64 KiB of dynamic LDS: raise the kernel's limit once
-    static const hipError_t attr_gate = hipFuncSetAttribute((const void *) mc_mmq_gemm_kernel<T, true>,
-        hipFuncAttributeMaxDynamicSharedMemorySize, (int) (2 * (2 * WT + MMQ_MAX_BLOCKS * MMQ_REC_BYTES + 1024u)));
-    static const hipError_t attr_plain = hipFuncSetAttribute((const void *) mc_mmq_gemm_kernel<T, false>,
-        hipFuncAttributeMaxDynamicSharedMemorySize, (int) (2 * (WT + MMQ_MAX_BLOCKS * MMQ_REC_BYTES + 1024u)));
+    static const hipError_t attr_gate = hipFuncSetAttribute((const void *) mc_mmq_gemm_kernel<T, true, MAXB>,
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int) (2 * (2 * WT + MAXB * MMQ_REC_BYTES + 1024u)));
+    static const hipError_t attr_plain = hipFuncSetAttribute((const void *) mc_mmq_gemm_kernel<T, false, MAXB>,
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int) (2 * (WT + MAXB * MMQ_REC_BYTES + 1024u)));
     if (attr_gate != hipSuccess) return attr_gate;
     if (attr_plain != hipSuccess) return attr_plain;
-    if (gate) hipLaunchKernelGGL((mc_mmq_gemm_kernel<T, true>), grid, dim3(MMQ_WAVES * WAVE), 2 * stage, s, a);
-    else hipLaunchKernelGGL((mc_mmq_gemm_kernel<T, false>), grid, dim3(MMQ_WAVES * WAVE), 2 * stage, s, a);
+    if (gate) hipLaunchKernelGGL((mc_mmq_gemm_kernel<T, true, MAXB>), grid, dim3(MMQ_WAVES * WAVE), 2 * stage, s, a);
+    else hipLaunchKernelGGL((mc_mmq_gemm_kernel<T, false, MAXB>), grid, dim3(MMQ_WAVES * WAVE), 2 * stage, s, a);
     return hipGetLastError();
+}
+
+template <int T>
+static hipError_t launch_mmq_t(const MmqArgs &a, hipStream_t s) {
+    const int64_t pairs = (int64_t) a.n_tok * a.n_used;
+    if (pairs <= (int64_t) MMQ_FEW_PAIRS * a.n_experts) return launch_mmq_tb<T, 1>(a, s);
+    return launch_mmq_tb<T, MMQ_MAX_BLOCKS>(a, s);
 }
 
 // Grouping, activation records and the grouped GEMM; a.ws holds the workspace.

@@ -59,6 +59,32 @@ def test_mul_mat_q_matches_ggml_cpu(torch_gpu, mc, O, wtype, E, K, R, n_tok, n_u
     assert np.all(got[~valid] == sentinel)
 
 
+@pytest.mark.parametrize("wtype", [10, 12, 13])
+def test_mul_mat_q_many_pairs_per_expert(torch_gpu, mc, O, wtype):
+    """Experts with many pairs: more than MMQ_FEW_PAIRS per expert on average selects the
+    4-blocks-per-pass kernel, and expert 0 (every token's first slot) needs two passes."""
+    torch = torch_gpu
+    E, K, R, n_tok, n_used = 8, 1024, 136, 96, 2
+    _note(f"mul_mat_q many pairs type={wtype}")
+    w = H.weights(wtype, E, R, K, seed=1300 + wtype)
+    x = H.activations(n_tok, K, seed=1301)
+    ids = H.routing(n_tok, n_used, E, seed=1302)
+    ids[:, 1] = np.where(ids[:, 0] == 0, ids[:, 1], ids[:, 0])
+    ids[:, 1] = np.where(ids[:, 1] == 0, 1, ids[:, 1])
+    ids[:, 0] = 0
+    counts = np.bincount(ids.reshape(-1), minlength=E)
+    _note(f"  pairs per expert: {counts.tolist()}")
+    assert counts[0] == n_tok and counts.sum() == n_tok * n_used
+    dst = torch.zeros((n_tok, n_used, R), dtype=torch.float32, device="cuda")
+    mc.mul_mat_q(wtype=wtype, weights=_dev(torch, w), ids=_dev(torch, ids), y=_q8_K_rows(torch, mc, x), dst=dst, K=K,
+                 R=R, n_experts=E)
+    torch.cuda.synchronize()
+    want = O.cpu_mul_mat_id_f32(wtype=wtype, K=K, R=R, n_as=E, src0=w, src1=x, ids=ids)
+    err = O.rel_l2(dst.cpu().numpy(), want)
+    _note(f"  rel_l2 vs ggml-cpu={err:.3e}")
+    assert err <= H.TOL_SAME
+
+
 @pytest.mark.parametrize("wtype,R", [(12, 136), (10, 100)])
 def test_mul_mat_q_gate_glu(torch_gpu, mc, O, wtype, R):
     torch = torch_gpu
