@@ -10,7 +10,8 @@
 // super-block then accumulate exactly in int32, with one float update per
 // super-block.  Q4_K/Q5_K scale each 32-value MFMA result by its 6-bit
 // sub-block scale; Q2_K (16-value groups) folds its 4-bit scales into the
-// weight codes and takes the min term from a second MFMA.
+// weight codes and takes the min term from a second MFMA; Q6_K (16-value
+// groups, int8 scales) splits each sub-block into one MFMA per group.
 //
 // Three launches:
 //   1. mc_mmq_group_kernel  (one workgroup): pair counts per expert, offsets,
@@ -185,27 +186,47 @@ __global__ __launch_bounds__(256) void mc_mmq_pack_kernel(const MmqArgs a) {
 // 3. grouped GEMM
 // ---------------------------------------------------------------------------
 
-// Bytes per lane of the weight-tile DMA: 16 where a super-block is a whole number of
-// 16-byte chunks (Q4_K 144, Q5_K 176), else 4 (Q2_K 84: 21 dwords).
+// LDS tile geometry of one row's super-block and the DMA pieces that fill it:
+//   Q4_K/Q5_K (144/176 B): 16-byte pieces, rows back to back;
+//   Q2_K (84 B): dword pieces, rows back to back;
+//   Q6_K (210 B, a row's super-blocks only 2-byte aligned in memory): the dword-
+//   aligned 212-byte window around each super-block, rows back to back; the
+//   super-block starts sh = (its address & 3) bytes into its window (0 or 2), and
+//   the decode reads its words with byte alignment (v_alignbyte).  The window's
+//   extra two bytes belong to a neighbouring super-block (or read as zeros past
+//   the buffer) and are never used.  (Buffer->LDS DMA of 1- or 2-byte pieces writes
+//   one dword per lane, so it cannot pack 2-byte aligned rows.)
 template <int T>
-constexpr int mmq_dma_bytes() { return type_geom(T).block_bytes % 16 == 0 ? 16 : 4; }
+struct MmqTile {
+    static constexpr int SBB = type_geom(T).block_bytes;
+    static constexpr bool WIN = SBB % 4 != 0;
+    static constexpr int DB = SBB % 16 == 0 ? 16 : 4;                  // bytes per lane and DMA
+    static constexpr int RP = WIN ? SBB + 2 : SBB;                      // LDS row pitch
+    static constexpr int CH = RP / DB;                                  // pieces per row
+    static constexpr int N_INS = MMQ_ROWS * RP / (WAVE * DB);           // wave DMA instructions per tile
+    static constexpr uint32_t WT = MMQ_ROWS * RP;                       // LDS tile bytes
+    static_assert(!WIN || SBB % 4 == 2, "windows cover super-blocks that are 2-byte aligned");
+    static_assert(MMQ_ROWS * RP % (WAVE * DB) == 0, "whole DMA instructions per tile");
+};
 
-// Issues the DMA of super-block s: MMQ_ROWS weight rows (one super-block each,
-// rows row_bytes apart, landing back to back in LDS) and nb activation records.
+// Issues the DMA of super-block s: MMQ_ROWS weight rows (one super-block, or its
+// window, each; rows row_bytes apart in memory, back to back in LDS) and nb
+// activation records.
 template <int T>
 __device__ __forceinline__ void mmq_issue(const MmqArgs &a, const uint8_t *wbase, int row0, int s, int blk0, int nb,
                                           uint8_t *wl, uint8_t *rl) {
-    constexpr int SBB = type_geom(T).block_bytes;           // bytes of one super-block
-    constexpr int DB = mmq_dma_bytes<T>();
-    constexpr int CH = SBB / DB;                            // DMA chunks per super-block
+    using G = MmqTile<T>;
     const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-    const uint32_t row_bytes = (uint32_t) (a.ncols / 256) * SBB;
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(wbase, (uint32_t) a.expert_bytes);
-    for (int i = wave; i < CH * MMQ_ROWS / WAVE; i += MMQ_WAVES) {
-        const int q = i * WAVE + lane;                       // chunk q of the tile: row q / CH, part q % CH
-        const uint32_t off = (uint32_t) (row0 + q / CH) * row_bytes + (uint32_t) s * SBB + (uint32_t) DB * (uint32_t) (q % CH);
-        if constexpr (DB == 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void_t *) (wl + WAVE * DB * i), 16, off, 0, 0, 0);
-        else __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void_t *) (wl + WAVE * DB * i), 4, off, 0, 0, 0);
+    const uint32_t row_bytes = (uint32_t) (a.ncols / 256) * G::SBB;
+    const uint32_t b0 = (uint32_t) ((uintptr_t) wbase & 3u);     // 0 except for a 2-byte aligned Q6_K expert
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(wbase - b0, (uint32_t) a.expert_bytes + b0);
+    for (int i = wave; i < G::N_INS; i += MMQ_WAVES) {
+        const int q = i * WAVE + lane;                       // piece q of the tile: row q / CH, part q % CH
+        const uint32_t o = b0 + (uint32_t) (row0 + q / G::CH) * row_bytes + (uint32_t) s * G::SBB;
+        const uint32_t off = (G::WIN ? (o & ~3u) : o) + (uint32_t) G::DB * (uint32_t) (q % G::CH);
+        lds_void_t *dst = (lds_void_t *) (wl + WAVE * G::DB * i);
+        if constexpr (G::DB == 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, dst, 16, off, 0, 0, 0);
+        else __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, dst, 4, off, 0, 0, 0);
     }
     if (nb <= 0) return;
     const uint8_t *recs = a.ws + a.ws_packed + ((int64_t) s * a.max_blocks + blk0) * MMQ_REC_BYTES;
@@ -215,9 +236,9 @@ __device__ __forceinline__ void mmq_issue(const MmqArgs &a, const uint8_t *wbase
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void_t *) (rl + 1024 * i), 16, 1024u * i + 16u * lane, 0, 0, 0);
 }
 
-__device__ __forceinline__ int mmq_issue_count(int nb, int wave, int ch) {
+__device__ __forceinline__ int mmq_issue_count(int nb, int wave, int n_ins) {
     int n = 0;
-    for (int i = wave; i < ch * MMQ_ROWS / WAVE; i += MMQ_WAVES) ++n;
+    for (int i = wave; i < n_ins; i += MMQ_WAVES) ++n;
     for (int i = wave; i < (nb * MMQ_REC_BYTES + 1023) / 1024; i += MMQ_WAVES) ++n;
     return n;
 }
@@ -409,12 +430,109 @@ __device__ __forceinline__ void mmq_superblock_q2K(const uint8_t *wrow_up, const
     }
 }
 
+// Q6_K row super-block (ql[128], qh[64], scales[16] int8, d) sh bytes into its LDS
+// window w.  Element 128 n + 32 j + l (n = 0, 1; j = 0..3; l = 0..31) is
+//   ((ql[64 n + 32 (j & 1) + l] >> 4 (j >> 1)) & 15 | ((qh[32 n + l] >> 2 j) & 3) << 4) - 32
+// in 16-value group 8 n + 2 j + l / 16.  B fragment of sub-block 4 n + j for this lane
+// (values 8 kq .. 8 kq + 7): the eight codes as int8.  code - 32 is the code with
+// bit 5 flipped read as a 6-bit two's complement number, so it is sign-extended
+// from bit 5 (bits 6 and 7 set where bit 5 is), bytewise without carries.
+__device__ __forceinline__ u32 win_word(const u32 *w, u32 sh, int k) {
+    // word k of a super-block that starts sh bytes into the dword-aligned window w
+    return __builtin_amdgcn_alignbyte(w[k + 1], w[k], sh);
+}
+
+__device__ __forceinline__ long q6K_codes(const u32 *w, u32 sh, int n, int j, int kq) {
+    const int qlw = 16 * n + 8 * (j & 1) + 2 * kq;          // ql word of values 8 kq ..
+    const int qhw = 32 + 8 * n + 2 * kq;                    // qh word (qh starts at byte 128)
+    u32 r[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const u32 lo = (win_word(w, sh, qlw + h) >> (4 * (j >> 1))) & 0x0F0F0F0Fu;
+        const u32 hi = ((win_word(w, sh, qhw + h) >> (2 * j)) & 0x03030303u) << 4;
+        const u32 t = (lo | hi) ^ 0x20202020u;
+        const u32 sgn = t & 0x20202020u;
+        r[h] = t | (sgn << 1) | (sgn << 2);
+    }
+    return (long) (((uint64_t) r[1] << 32) | r[0]);
+}
+
+// Q6_K: one super-block of the wave's 16-row tile against nb column blocks.  A lane's
+// eight values share one 16-value group (even for kq < 2, odd otherwise), so each
+// 32-value sub-block takes two MFMAs, one with only the even group's lanes and one
+// with only the odd group's, each scaled by its group's int8 scale; no min term.
+// A window that starts on its super-block (sh = 0) ends two bytes past it; at the very
+// end of a matrix those bytes lie outside the buffer, and the DMA returns the whole
+// last dword (d and the two bytes) as zeros.  For that super-block (tail) d is read
+// from memory instead: gup / ggt point at the super-block's bytes in the up / gate
+// matrix.
+template <bool GATE, int MAXB>
+__device__ __forceinline__ void mmq_superblock_q6K(const uint8_t *wrow_up, const uint8_t *wrow_gate, u32 sh,
+                                                   bool tail, const uint8_t *gup, const uint8_t *ggt,
+                                                   const uint8_t *recs, int nb, float (&acc)[MAXB][4],
+                                                   float (&accg)[MAXB][4]) {
+    const int lane = threadIdx.x % WAVE;
+    const int kq = lane / 16;
+    const bool even = kq < 2;
+    const u32 *wu = (const u32 *) wrow_up;
+    const u32 *wg = (const u32 *) wrow_gate;
+    long cu[8], cg[8];
+    int seu[8], sou[8], seg[8], sog[8];
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int sb = 4 * n + j;
+            // scales[8 n + 2 j] and [8 n + 2 j + 1]: bytes 2 (j & 1) and 2 (j & 1) + 1 of word 48 + 2 n + j / 2
+            cu[sb] = q6K_codes(wu, sh, n, j, kq);
+            const u32 su = win_word(wu, sh, 48 + 2 * n + (j >> 1)) >> (16 * (j & 1));
+            seu[sb] = (int) (int8_t) (su & 0xFFu);
+            sou[sb] = (int) (int8_t) ((su >> 8) & 0xFFu);
+            if constexpr (GATE) {
+                cg[sb] = q6K_codes(wg, sh, n, j, kq);
+                const u32 sg = win_word(wg, sh, 48 + 2 * n + (j >> 1)) >> (16 * (j & 1));
+                seg[sb] = (int) (int8_t) (sg & 0xFFu);
+                sog[sb] = (int) (int8_t) ((sg >> 8) & 0xFFu);
+            }
+        }
+    // d: bytes 208..209
+    const float du = h2f(tail ? (u32) * (const uint16_t *) (gup + 208) : win_word(wu, sh, 52));
+    const float dg = GATE ? h2f(tail ? (u32) * (const uint16_t *) (ggt + 208) : win_word(wg, sh, 52)) : 0.0f;
+#pragma unroll
+    for (int b = 0; b < MAXB; ++b) {
+        if (b >= nb) break;
+        const uint8_t *rec = recs + b * MMQ_REC_BYTES;
+        const long *af = (const long *) (rec + MMQ_REC_FRAG);
+        int iu[4] = {0, 0, 0, 0}, ig[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int sb = 0; sb < 8; ++sb) {
+            const long a = af[sb * 64 + lane];
+            const v4i ue = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, even ? cu[sb] : 0l, v4i{0, 0, 0, 0}, 0, 0, 0);
+            const v4i uo = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, even ? 0l : cu[sb], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) iu[i] += __mul24(seu[sb], ue[i]) + __mul24(sou[sb], uo[i]);
+            if constexpr (GATE) {
+                const v4i ge = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, even ? cg[sb] : 0l, v4i{0, 0, 0, 0}, 0, 0, 0);
+                const v4i go = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, even ? 0l : cg[sb], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ig[i] += __mul24(seg[sb], ge[i]) + __mul24(sog[sb], go[i]);
+            }
+        }
+        const v4f d8 = *(const v4f *) (rec + MMQ_REC_D8 + 16 * kq);
+        const float d8a[4] = {d8.x, d8.y, d8.z, d8.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc[b][i] += mmq_superblock_value(d8a[i], du, 0.0f, iu[i], 0);
+            if constexpr (GATE) accg[b][i] += mmq_superblock_value(d8a[i], dg, 0.0f, ig[i], 0);
+        }
+    }
+}
+
 template <int T, bool GATE, int MAXB>
 __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const MmqArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    constexpr int SBB = type_geom(T).block_bytes;
-    constexpr int CH = SBB / mmq_dma_bytes<T>();
-    constexpr uint32_t WT = MMQ_ROWS * SBB;                 // weight tile bytes per matrix and super-block
+    constexpr int N_INS = MmqTile<T>::N_INS;
+    constexpr uint32_t WT = MmqTile<T>::WT;                 // weight tile bytes per matrix and super-block
     const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
     const int e = blockIdx.y;
     const int *blk_off = (const int *) (a.ws + a.ws_blk_off);
@@ -436,7 +554,7 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
         for (int b = 0; b < MAXB; ++b)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[b][i] = accg[b][i] = 0.0f;
-        const int per_stage = mmq_issue_count(nb, wave, CH) + (GATE ? mmq_issue_count(0, wave, CH) : 0);
+        const int per_stage = mmq_issue_count(nb, wave, N_INS) + (GATE ? mmq_issue_count(0, wave, N_INS) : 0);
         auto issue = [&](int s) {
             uint8_t *st = lds + (uint32_t) (s & 1) * stage;
             mmq_issue<T>(a, wup, row0, s, blk_first + g0, nb, st, st + (GATE ? 2 : 1) * WT);
@@ -453,8 +571,21 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
             lds_barrier();                                    // ... and for every wave (stage s + 1 stays in flight)
             const uint8_t *st = lds + (uint32_t) (s & 1) * stage;
             const uint8_t *recs = st + (GATE ? 2 : 1) * WT;
-            const uint32_t roff = (uint32_t) (16 * wave + lane % 16) * SBB;
+            const uint32_t roff = (uint32_t) (16 * wave + lane % 16) * MmqTile<T>::RP;
             if constexpr (T == T_Q2_K) mmq_superblock_q2K<GATE, MAXB>(st + roff, st + WT + roff, recs, nb, acc, accg);
+            else if constexpr (T == T_Q6_K) {
+                // where this row's super-block starts in its window: the same address
+                // arithmetic as mmq_issue (both matrices of an expert share it when the
+                // gate's base has the up's alignment, which the entry point checks)
+                const int wrow = row0 + 16 * wave + lane % 16;
+                const uint32_t b0 = (uint32_t) ((uintptr_t) wup & 3u);
+                const uint32_t rel = (uint32_t) wrow * (uint32_t) (n_sb * MmqTile<T>::SBB) + (uint32_t) s * MmqTile<T>::SBB;
+                const uint32_t sh = (b0 + rel) & 3u;
+                // rows past nrows (the last tile's padding) are never stored and never read from memory
+                const bool tail = wrow < a.nrows && sh == 0 && rel + MmqTile<T>::RP > (uint32_t) a.expert_bytes;
+                mmq_superblock_q6K<GATE, MAXB>(st + roff, st + WT + roff, sh, tail, wup + rel, GATE ? wgt + rel : nullptr,
+                                               recs, nb, acc, accg);
+            }
             else mmq_superblock<T, GATE, MAXB>(st + roff, st + WT + roff, recs, nb, acc, accg);
             lds_barrier();                                    // stage s is free for s + 2
         }
@@ -485,7 +616,7 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
 
 template <int T, int MAXB>
 static hipError_t launch_mmq_tb(const MmqArgs &a, hipStream_t s) {
-    constexpr uint32_t WT = MMQ_ROWS * type_geom(T).block_bytes;
+    constexpr uint32_t WT = MmqTile<T>::WT;
     const bool gate = a.w_gate != nullptr;
     const uint32_t stage = (gate ? 2u : 1u) * WT + MAXB * MMQ_REC_BYTES + 1024u;
     const dim3 grid((unsigned) ((a.nrows + MMQ_ROWS - 1) / MMQ_ROWS), (unsigned) a.n_experts);
@@ -522,6 +653,7 @@ int launch_mmq(const MmqArgs &a, int type, void *stream) {
     switch (type) {
         case T_Q2_K: return (int) launch_mmq_t<T_Q2_K>(a, s);
         case T_Q4_K: return (int) launch_mmq_t<T_Q4_K>(a, s);
+        case T_Q6_K: return (int) launch_mmq_t<T_Q6_K>(a, s);
         case T_Q5_K: return (int) launch_mmq_t<T_Q5_K>(a, s);
         default: return (int) hipErrorInvalidValue;
     }
