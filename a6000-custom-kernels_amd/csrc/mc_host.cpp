@@ -920,7 +920,7 @@ int ggml_hip_moe_mul_mat_q(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_f
     if (!src0 || !src0->data || !src1_q8_K || !ids_d || !dst_d || !workspace)
         return fail(E_INVALID, "mul_mat_q: null argument");
     const int tw = src0->type;
-    if (tw != T_Q2_K && tw != T_Q4_K && tw != T_Q5_K && tw != T_Q6_K)
+    if (tw != T_Q2_K && tw != T_Q3_K && tw != T_Q4_K && tw != T_Q5_K && tw != T_Q6_K)
         return fail(E_UNSUPPORTED, "mul_mat_q: expert type %d is not supported", tw);
     if (ne00 <= 0 || ne00 % 256 || ne01 <= 0 || ne02 <= 0 || ncols_dst <= 0 || nchannels_dst <= 0 || nchannels_y <= 0)
         return fail(E_INVALID, "mul_mat_q: bad shape");
@@ -934,12 +934,13 @@ int ggml_hip_moe_mul_mat_q(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_f
     const uint64_t eb = (uint64_t) src0->nb[2];
     if (eb > 0xFFFFFFF0ull) return fail(E_UNSUPPORTED, "mul_mat_q: expert matrix larger than 4 GiB");
     // the weight tiles are fetched in 16-byte pieces (Q4_K/Q5_K), dwords (Q2_K) or dword windows
-    // around 2-byte aligned super-blocks (Q6_K: the gate must share the up matrix's alignment)
-    const uintptr_t walign = tw == T_Q6_K ? 1u : tw == T_Q2_K ? 3u : 15u;
+    // around 2-byte aligned super-blocks (Q3_K/Q6_K: the gate must share the up matrix's alignment)
+    const bool windows = tw == T_Q3_K || tw == T_Q6_K;
+    const uintptr_t walign = windows ? 1u : tw == T_Q2_K ? 3u : 15u;
     if (((uintptr_t) src0->data | eb | (uintptr_t) (fusion ? fusion->gate : nullptr)) & walign)
         return fail(E_UNSUPPORTED, "mul_mat_q: expert weights must be %d-byte aligned", (int) walign + 1);
-    if (tw == T_Q6_K && fusion && fusion->gate && (((uintptr_t) fusion->gate ^ (uintptr_t) src0->data) & 3u))
-        return fail(E_UNSUPPORTED, "mul_mat_q: Q6_K gate and up matrices must share their address mod 4");
+    if (windows && fusion && fusion->gate && (((uintptr_t) fusion->gate ^ (uintptr_t) src0->data) & 3u))
+        return fail(E_UNSUPPORTED, "mul_mat_q: Q3_K/Q6_K gate and up matrices must share their address mod 4");
     if (((uintptr_t) src1_q8_K | (uintptr_t) workspace) & 255u)
         return fail(E_INVALID, "mul_mat_q: activations and workspace must be 256-byte aligned");
     MmqArgs a = {};

@@ -10,8 +10,8 @@
 // super-block then accumulate exactly in int32, with one float update per
 // super-block.  Q4_K/Q5_K scale each 32-value MFMA result by its 6-bit
 // sub-block scale; Q2_K (16-value groups) folds its 4-bit scales into the
-// weight codes and takes the min term from a second MFMA; Q6_K (16-value
-// groups, int8 scales) splits each sub-block into one MFMA per group.
+// weight codes and takes the min term from a second MFMA; Q3_K and Q6_K
+// (16-value groups, signed scales) split each sub-block into one MFMA per group.
 //
 // Three launches:
 //   1. mc_mmq_group_kernel  (one workgroup): pair counts per expert, offsets,
@@ -189,8 +189,8 @@ __global__ __launch_bounds__(256) void mc_mmq_pack_kernel(const MmqArgs a) {
 // LDS tile geometry of one row's super-block and the DMA pieces that fill it:
 //   Q4_K/Q5_K (144/176 B): 16-byte pieces, rows back to back;
 //   Q2_K (84 B): dword pieces, rows back to back;
-//   Q6_K (210 B, a row's super-blocks only 2-byte aligned in memory): the dword-
-//   aligned 212-byte window around each super-block, rows back to back; the
+//   Q3_K / Q6_K (110 / 210 B, a row's super-blocks only 2-byte aligned in memory):
+//   the dword-aligned 112 / 212-byte window around each super-block, rows back to back; the
 //   super-block starts sh = (its address & 3) bytes into its window (0 or 2), and
 //   the decode reads its words with byte alignment (v_alignbyte).  The window's
 //   extra two bytes belong to a neighbouring super-block (or read as zeros past
@@ -461,16 +461,72 @@ __device__ __forceinline__ long q6K_codes(const u32 *w, u32 sh, int n, int j, in
 // eight values share one 16-value group (even for kq < 2, odd otherwise), so each
 // 32-value sub-block takes two MFMAs, one with only the even group's lanes and one
 // with only the odd group's, each scaled by its group's int8 scale; no min term.
+// Q3_K row super-block (hmask[32], qs[64], scales[12], d) sh bytes into its LDS window
+// w.  Element 128 h + 32 j + l (h = 0, 1; j = 0..3; l = 0..31) is
+//   ((qs[32 h + l] >> 2 j) & 3) - ((hmask[l] >> (4 h + j)) & 1 ? 0 : 4)
+// in 16-value group 8 h + 2 j + l / 16.  B fragment of sub-block 4 h + j for this lane:
+// the eight codes as int8: (low | high << 2) ^ 4 is the code's 3-bit two's complement,
+// sign-extended from bit 2 (bits 3..7 set where bit 2 is, bytewise without carries).
+__device__ __forceinline__ long q3K_codes(const u32 *w, u32 sh, int h, int j, int kq) {
+    u32 r[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const u32 lo = (win_word(w, sh, 8 + 8 * h + 2 * kq + i) >> (2 * j)) & 0x03030303u;   // qs at byte 32
+        const u32 hb = (win_word(w, sh, 2 * kq + i) >> (4 * h + j)) & 0x01010101u;          // hmask at byte 0
+        const u32 t = (lo | (hb << 2)) ^ 0x04040404u;
+        r[i] = t | ((t & 0x04040404u) * 62u);
+    }
+    return (long) (((uint64_t) r[1] << 32) | r[0]);
+}
+
+// The 6-bit scale of 16-value group g (ggml's Q3_K packing: low nibbles in bytes
+// 0..7, two high bits per scale in bytes 8..11), offset by -32.
+__device__ __forceinline__ int q3K_scale(const u32 *w, u32 sh, int g) {
+    const u32 a03 = win_word(w, sh, 24), a47 = win_word(w, sh, 25), a8b = win_word(w, sh, 26);   // scales at byte 96
+    const u32 lw = (g & 7) < 4 ? a03 : a47;
+    const u32 lo = (lw >> (8 * (g & 3) + 4 * (g >> 3))) & 0xFu;
+    const u32 hi = (a8b >> (8 * (g & 3) + 2 * (g >> 2))) & 3u;
+    return (int) (lo | (hi << 4)) - 32;
+}
+
+// The B fragment (codes) and the even / odd group scales of sub-block sb for a
+// 16-value-group type whose super-blocks arrive in windows (Q3_K, Q6_K).
+template <int T>
+__device__ __forceinline__ void g16_subblock(const u32 *w, u32 sh, int sb, int kq, long &codes, int &se, int &so) {
+    const int n = sb >> 2, j = sb & 3;
+    if constexpr (T == T_Q6_K) {
+        // scales[8 n + 2 j] and [8 n + 2 j + 1]: bytes 2 (j & 1) and 2 (j & 1) + 1 of word 48 + 2 n + j / 2
+        codes = q6K_codes(w, sh, n, j, kq);
+        const u32 sw = win_word(w, sh, 48 + 2 * n + (j >> 1)) >> (16 * (j & 1));
+        se = (int) (int8_t) (sw & 0xFFu);
+        so = (int) (int8_t) ((sw >> 8) & 0xFFu);
+    } else {
+        codes = q3K_codes(w, sh, n, j, kq);
+        se = q3K_scale(w, sh, 8 * n + 2 * j);
+        so = q3K_scale(w, sh, 8 * n + 2 * j + 1);
+    }
+}
+
+// Byte offset of d in a super-block of a 16-value-group type.
+template <int T>
+constexpr int g16_d_offset() { return T == T_Q6_K ? 208 : 108; }
+
 // A window that starts on its super-block (sh = 0) ends two bytes past it; at the very
 // end of a matrix those bytes lie outside the buffer, and the DMA returns the whole
 // last dword (d and the two bytes) as zeros.  For that super-block (tail) d is read
 // from memory instead: gup / ggt point at the super-block's bytes in the up / gate
 // matrix.
-template <bool GATE, int MAXB>
-__device__ __forceinline__ void mmq_superblock_q6K(const uint8_t *wrow_up, const uint8_t *wrow_gate, u32 sh,
+//
+// Q3_K / Q6_K: one super-block of the wave's 16-row tile against nb column blocks.  A
+// lane's eight values share one 16-value group (even for kq < 2, odd otherwise), so
+// each 32-value sub-block takes two MFMAs, one with only the even group's lanes and
+// one with only the odd group's, each scaled by its group's scale; no min term.
+template <int T, bool GATE, int MAXB>
+__device__ __forceinline__ void mmq_superblock_g16(const uint8_t *wrow_up, const uint8_t *wrow_gate, u32 sh,
                                                    bool tail, const uint8_t *gup, const uint8_t *ggt,
                                                    const uint8_t *recs, int nb, float (&acc)[MAXB][4],
                                                    float (&accg)[MAXB][4]) {
+    constexpr int DO = g16_d_offset<T>();
     const int lane = threadIdx.x % WAVE;
     const int kq = lane / 16;
     const bool even = kq < 2;
@@ -479,25 +535,12 @@ __device__ __forceinline__ void mmq_superblock_q6K(const uint8_t *wrow_up, const
     long cu[8], cg[8];
     int seu[8], sou[8], seg[8], sog[8];
 #pragma unroll
-    for (int n = 0; n < 2; ++n)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int sb = 4 * n + j;
-            // scales[8 n + 2 j] and [8 n + 2 j + 1]: bytes 2 (j & 1) and 2 (j & 1) + 1 of word 48 + 2 n + j / 2
-            cu[sb] = q6K_codes(wu, sh, n, j, kq);
-            const u32 su = win_word(wu, sh, 48 + 2 * n + (j >> 1)) >> (16 * (j & 1));
-            seu[sb] = (int) (int8_t) (su & 0xFFu);
-            sou[sb] = (int) (int8_t) ((su >> 8) & 0xFFu);
-            if constexpr (GATE) {
-                cg[sb] = q6K_codes(wg, sh, n, j, kq);
-                const u32 sg = win_word(wg, sh, 48 + 2 * n + (j >> 1)) >> (16 * (j & 1));
-                seg[sb] = (int) (int8_t) (sg & 0xFFu);
-                sog[sb] = (int) (int8_t) ((sg >> 8) & 0xFFu);
-            }
-        }
-    // d: bytes 208..209
-    const float du = h2f(tail ? (u32) * (const uint16_t *) (gup + 208) : win_word(wu, sh, 52));
-    const float dg = GATE ? h2f(tail ? (u32) * (const uint16_t *) (ggt + 208) : win_word(wg, sh, 52)) : 0.0f;
+    for (int sb = 0; sb < 8; ++sb) {
+        g16_subblock<T>(wu, sh, sb, kq, cu[sb], seu[sb], sou[sb]);
+        if constexpr (GATE) g16_subblock<T>(wg, sh, sb, kq, cg[sb], seg[sb], sog[sb]);
+    }
+    const float du = h2f(tail ? (u32) * (const uint16_t *) (gup + DO) : win_word(wu, sh, DO / 4));
+    const float dg = GATE ? h2f(tail ? (u32) * (const uint16_t *) (ggt + DO) : win_word(wg, sh, DO / 4)) : 0.0f;
 #pragma unroll
     for (int b = 0; b < MAXB; ++b) {
         if (b >= nb) break;
@@ -573,7 +616,7 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
             const uint8_t *recs = st + (GATE ? 2 : 1) * WT;
             const uint32_t roff = (uint32_t) (16 * wave + lane % 16) * MmqTile<T>::RP;
             if constexpr (T == T_Q2_K) mmq_superblock_q2K<GATE, MAXB>(st + roff, st + WT + roff, recs, nb, acc, accg);
-            else if constexpr (T == T_Q6_K) {
+            else if constexpr (MmqTile<T>::WIN) {
                 // where this row's super-block starts in its window: the same address
                 // arithmetic as mmq_issue (both matrices of an expert share it when the
                 // gate's base has the up's alignment, which the entry point checks)
@@ -583,8 +626,8 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
                 const uint32_t sh = (b0 + rel) & 3u;
                 // rows past nrows (the last tile's padding) are never stored and never read from memory
                 const bool tail = wrow < a.nrows && sh == 0 && rel + MmqTile<T>::RP > (uint32_t) a.expert_bytes;
-                mmq_superblock_q6K<GATE, MAXB>(st + roff, st + WT + roff, sh, tail, wup + rel, GATE ? wgt + rel : nullptr,
-                                               recs, nb, acc, accg);
+                mmq_superblock_g16<T, GATE, MAXB>(st + roff, st + WT + roff, sh, tail, wup + rel,
+                                                  GATE ? wgt + rel : nullptr, recs, nb, acc, accg);
             }
             else mmq_superblock<T, GATE, MAXB>(st + roff, st + WT + roff, recs, nb, acc, accg);
             lds_barrier();                                    // stage s is free for s + 2
@@ -652,6 +695,7 @@ int launch_mmq(const MmqArgs &a, int type, void *stream) {
     if ((err = hipGetLastError()) != hipSuccess) return (int) err;
     switch (type) {
         case T_Q2_K: return (int) launch_mmq_t<T_Q2_K>(a, s);
+        case T_Q3_K: return (int) launch_mmq_t<T_Q3_K>(a, s);
         case T_Q4_K: return (int) launch_mmq_t<T_Q4_K>(a, s);
         case T_Q6_K: return (int) launch_mmq_t<T_Q6_K>(a, s);
         case T_Q5_K: return (int) launch_mmq_t<T_Q5_K>(a, s);

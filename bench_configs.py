@@ -10,8 +10,8 @@
          seeded routings per point;
   cfg5a  the prefill-shaped FFN: 512 tokens x top-8 over 512 Q4_K experts through
          the expert-grouped int8-MFMA path (q8_K of x, gate/up + SwiGLU, q8_K of
-         the GLU rows, down); cfg5a_q2K / cfg5a_q6K: the same shape over Q2_K / Q6_K
-         experts;
+         the GLU rows, down); cfg5a_q2K / _q3K / _q6K: the same shape over Q2_K /
+         Q3_K / Q6_K experts;
   ssm_conv  SSM_CONV with F16 taps and the fused bias + SiLU (d_conv 4, d_inner
          8192): 512-token prefill and one-token decode;
   cfg3   the pointer-table cache under mixed residency: 40 layers of Q2_K experts
@@ -25,7 +25,8 @@ expert matrices a launch touches plus activations and outputs.  cpu_baseline
 (cfg1) is the CPU oracle's ggml-CPU MUL_MAT_ID restatement on this host; the
 ssm_conv line carries the oracle's single-thread SSM_CONV on the same input.
 
-Usage: python bench_configs.py [--configs cfg1,cfg3,cfg4,cfg5a,cfg5a_q2K,cfg5a_q6K,ssm_conv] [--rounds N]
+Usage: python bench_configs.py [--configs cfg1,cfg3,cfg4,cfg5a,cfg5a_q2K,cfg5a_q3K,cfg5a_q6K,ssm_conv]
+                               [--rounds N]
 """
 from __future__ import annotations
 
@@ -194,7 +195,7 @@ def prefill_ffn(torch, mc, md, rounds, wtype, name):
     wbytes = touched * 3 * eb
     ops = 2 * T * U * 3 * F * H
     gbs = wbytes / (ms_all * 1e-3) / 1e9
-    tname = {mc.Q2_K: "Q2_K", mc.Q4_K: "Q4_K", mc.Q6_K: "Q6_K"}[wtype]
+    tname = {mc.Q2_K: "Q2_K", mc.Q3_K: "Q3_K", mc.Q4_K: "Q4_K", mc.Q6_K: "Q6_K"}[wtype]
     emit({"config": name, "workload": f"prefill FFN, 512 tokens x top-8 of 512 {tname} experts (hidden 4096, "
                                       "ffn 768), q8_K activations, int8 MFMA grouped GEMM",
           "us_per_layer": round(ms_all * 1000, 1), "us_gate_up": round(ms_gu * 1000, 1),
@@ -245,6 +246,11 @@ def cfg5a(torch, mc, md, rounds):
 def cfg5a_q2K(torch, mc, md, rounds):
     """The same prefill shape over Q2_K experts (the decode model's routed type)."""
     prefill_ffn(torch, mc, md, rounds, mc.Q2_K, "cfg5a_q2K")
+
+
+def cfg5a_q3K(torch, mc, md, rounds):
+    """The same prefill shape over Q3_K experts."""
+    prefill_ffn(torch, mc, md, rounds, mc.Q3_K, "cfg5a_q3K")
 
 
 def cfg5a_q6K(torch, mc, md, rounds):
@@ -398,7 +404,7 @@ def cfg3(torch, mc, md, rounds, tokens=256, calib_tokens=32, layers=40):
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--configs", default="cfg1,cfg4,cfg5a,cfg5a_q2K,cfg5a_q6K,ssm_conv")
+    ap.add_argument("--configs", default="cfg1,cfg4,cfg5a,cfg5a_q2K,cfg5a_q3K,cfg5a_q6K,ssm_conv")
     ap.add_argument("--rounds", type=int, default=10)
     args = ap.parse_args()
     import torch
@@ -407,7 +413,8 @@ def main():
     assert torch.cuda.is_available(), "bench_configs.py needs a HIP device"
     for name in args.configs.split(","):
         log(f"running {name}")
-        {"cfg1": cfg1, "cfg3": cfg3, "cfg4": cfg4, "cfg5a": cfg5a, "cfg5a_q2K": cfg5a_q2K, "cfg5a_q6K": cfg5a_q6K,
+        {"cfg1": cfg1, "cfg3": cfg3, "cfg4": cfg4, "cfg5a": cfg5a, "cfg5a_q2K": cfg5a_q2K, "cfg5a_q3K": cfg5a_q3K,
+         "cfg5a_q6K": cfg5a_q6K,
          "ssm_conv": ssm_conv}[name](torch, mc, md, args.rounds)
 
 

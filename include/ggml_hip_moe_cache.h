@@ -273,14 +273,14 @@ int ggml_hip_moe_ffn_down_combine(
  * experts and n_pairs = tokens * slots (no initialisation required). */
 int64_t ggml_hip_moe_mul_mat_q_workspace_bytes(int64_t ne00, int64_t ne02, int64_t n_pairs);
 
-/* MUL_MAT_ID over device-resident K-quant experts (Q2_K, Q4_K, Q5_K, Q6_K) with q8_K
+/* MUL_MAT_ID over device-resident K-quant experts (Q2_K..Q6_K) with q8_K
  * activations (ggml_hip_quantize_q8_K; the ggml-CPU vec_dot_type of these types):
  *   dst[t*stride_col_dst + c*stride_channel_dst + r] = W[ids[c + t*ids_stride]][r] . y(t, c)
  * with y(t, c) the q8_K row (c % nchannels_y)*stride_channel_y + t*stride_col_y (strides in
  * q8_K blocks of 256 values).  fusion may carry gate (same shape, device) with glu_op/glu_limit:
  * dst = GLU(gate . y, W . y); other fusion fields are not supported here.  Expert ids outside
  * [0, ne02) are skipped.  src1 and workspace 256-byte aligned, weights 16-byte aligned
- * (Q2_K: 4-byte, Q6_K: 2-byte). */
+ * (Q2_K: 4-byte, Q3_K/Q6_K: 2-byte, a gate at the up matrix's address mod 4). */
 int ggml_hip_moe_mul_mat_q(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_fusion *fusion,
                            const void *src1_q8_K, const int32_t *ids_d, float *dst_d,
                            int64_t ne00, int64_t ne01, int64_t ne02,

@@ -28,9 +28,9 @@ def _q8_K_rows(torch, mc, x):
     return buf
 
 
-@pytest.mark.parametrize("wtype", [10, 12, 13, 14])
-# (16, 768, 101, ...): three super-blocks per row and an odd row count, so Q6_K rows and
-# experts alternate between 4-byte and 2-byte aligned starts
+@pytest.mark.parametrize("wtype", [10, 11, 12, 13, 14])
+# (16, 768, 101, ...): three super-blocks per row and an odd row count, so Q3_K / Q6_K rows
+# and experts alternate between 4-byte and 2-byte aligned starts
 @pytest.mark.parametrize("E,K,R,n_tok,n_used", [(16, 512, 100, 40, 4), (16, 768, 101, 40, 4),
                                                 (64, 4096, 256, 96, 8)])
 def test_mul_mat_q_matches_ggml_cpu(torch_gpu, mc, O, wtype, E, K, R, n_tok, n_used):
@@ -62,7 +62,7 @@ def test_mul_mat_q_matches_ggml_cpu(torch_gpu, mc, O, wtype, E, K, R, n_tok, n_u
     assert np.all(got[~valid] == sentinel)
 
 
-@pytest.mark.parametrize("wtype", [10, 12, 13, 14])
+@pytest.mark.parametrize("wtype", [10, 11, 12, 13, 14])
 def test_mul_mat_q_many_pairs_per_expert(torch_gpu, mc, O, wtype):
     """Experts with many pairs: more than MMQ_FEW_PAIRS per expert on average selects the
     4-blocks-per-pass kernel, and expert 0 (every token's first slot) needs two passes."""
@@ -88,7 +88,7 @@ def test_mul_mat_q_many_pairs_per_expert(torch_gpu, mc, O, wtype):
     assert err <= H.TOL_SAME
 
 
-@pytest.mark.parametrize("wtype,R", [(12, 136), (10, 100), (14, 72)])
+@pytest.mark.parametrize("wtype,R", [(12, 136), (10, 100), (14, 72), (11, 80)])
 def test_mul_mat_q_gate_glu(torch_gpu, mc, O, wtype, R):
     torch = torch_gpu
     E, K, n_tok, n_used = 24, 1024, 48, 6
