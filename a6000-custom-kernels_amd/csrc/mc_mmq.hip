@@ -143,15 +143,19 @@ __global__ __launch_bounds__(MMQ_GROUP_THREADS) void mc_mmq_group_kernel(const M
 //   [4160, 4416)  S[16][8] int16: the pairs' 32-value code sums per sub-block
 constexpr int MMQ_REC_FRAG = 0, MMQ_REC_D8 = 4096, MMQ_REC_SUM = 4160;
 
+// One wave per record: lane l = col + 16 kq fills the A fragments of pair col, values
+// 8 kq .. 8 kq + 7 of every sub-block (for a fixed sub-block the 64 lanes write 512
+// contiguous bytes); the lanes with kq = 0 write the pair's scale and sums.
 __global__ __launch_bounds__(256) void mc_mmq_pack_kernel(const MmqArgs a) {
     const int n_sb = a.ncols / 256;
-    const int64_t gid = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;   // (block, column, super-block)
-    const int s = (int) (gid % n_sb);
-    const int64_t bc = gid / n_sb;
-    const int col = (int) (bc % MMQ_COLS);
-    const int b = (int) (bc / MMQ_COLS);
+    const int64_t gid = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;   // (super-block, block, lane)
+    const int lane = (int) (gid % WAVE);
+    const int64_t sb_b = gid / WAVE;
+    const int b = (int) (sb_b % a.max_blocks);
+    const int s = (int) (sb_b / a.max_blocks);
     const int *blk_off = (const int *) (a.ws + a.ws_blk_off);
-    if (b >= a.max_blocks || b >= blk_off[a.n_experts]) return;
+    if (s >= n_sb || b >= blk_off[a.n_experts]) return;
+    const int col = lane % MMQ_COLS, kq = lane / MMQ_COLS;
     const int *row = (const int *) (a.ws + a.ws_blk_tab) + 4 * b;
     uint8_t *rec = a.ws + a.ws_packed + ((int64_t) s * a.max_blocks + b) * MMQ_REC_BYTES;
     uint64_t *frag = (uint64_t *) (rec + MMQ_REC_FRAG);
@@ -159,12 +163,11 @@ __global__ __launch_bounds__(256) void mc_mmq_pack_kernel(const MmqArgs a) {
     int16_t *sums = (int16_t *) (rec + MMQ_REC_SUM) + 8 * col;
     if (col >= row[2]) {                      // empty column: zero codes, scale and sums
 #pragma unroll
-        for (int sb = 0; sb < 8; ++sb)
-#pragma unroll
-            for (int kq = 0; kq < 4; ++kq) frag[sb * 64 + col + 16 * kq] = 0;
-        d8[col] = 0.0f;
-#pragma unroll
-        for (int sb = 0; sb < 8; ++sb) sums[sb] = 0;
+        for (int sb = 0; sb < 8; ++sb) frag[sb * 64 + lane] = 0;
+        if (kq == 0) {
+            d8[col] = 0.0f;
+            *(v4u *) sums = v4u{0u, 0u, 0u, 0u};
+        }
         return;
     }
     const int p = ((const int *) (a.ws + a.ws_list))[row[1] + col];
@@ -173,13 +176,13 @@ __global__ __launch_bounds__(256) void mc_mmq_pack_kernel(const MmqArgs a) {
                          (int64_t) s * 292;
     const uint64_t *qs = (const uint64_t *) (blk + 4);     // q8_K: d (4 B) | qs[256] | bsums[16] int16
 #pragma unroll
-    for (int sb = 0; sb < 8; ++sb)
+    for (int sb = 0; sb < 8; ++sb) frag[sb * 64 + lane] = qs[4 * sb + kq];
+    if (kq == 0) {
+        d8[col] = *(const float *) blk;
+        const int16_t *bs = (const int16_t *) (blk + 260);
 #pragma unroll
-        for (int kq = 0; kq < 4; ++kq) frag[sb * 64 + col + 16 * kq] = qs[4 * sb + kq];
-    d8[col] = *(const float *) blk;
-    const int16_t *bs = (const int16_t *) (blk + 260);
-#pragma unroll
-    for (int sb = 0; sb < 8; ++sb) sums[sb] = (int16_t) (bs[2 * sb] + bs[2 * sb + 1]);
+        for (int sb = 0; sb < 8; ++sb) sums[sb] = (int16_t) (bs[2 * sb] + bs[2 * sb + 1]);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -690,7 +693,7 @@ int launch_mmq(const MmqArgs &a, int type, void *stream) {
     hipLaunchKernelGGL(mc_mmq_group_kernel, dim3(1), dim3(MMQ_GROUP_THREADS), 0, s, a);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return (int) err;
-    const int64_t threads = (int64_t) a.max_blocks * MMQ_COLS * (a.ncols / 256);
+    const int64_t threads = (int64_t) a.max_blocks * WAVE * (a.ncols / 256);
     hipLaunchKernelGGL(mc_mmq_pack_kernel, dim3((unsigned) ((threads + 255) / 256)), dim3(256), 0, s, a);
     if ((err = hipGetLastError()) != hipSuccess) return (int) err;
     switch (type) {
