@@ -112,6 +112,11 @@ SIGNATURES = [
     ("ggml_hip_moe_cache_stamps_snapshot", C.c_int, [_I32, _VP, _I32, _VP]),
     ("ggml_hip_moe_cache_totals", C.c_int, [C.POINTER(Totals)]),
     ("ggml_hip_moe_cache_reset", C.c_int, []),
+    ("ggml_hip_moe_mul_mat_id_workspace_bytes", C.c_int64,
+     [C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Fusion)]),
+    ("ggml_hip_moe_mul_mat_id", C.c_int,
+     [C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor),
+      C.POINTER(Fusion), _VP, _I64, _VP]),
     ("ggml_hip_ssm_conv_f32", C.c_int,
      [_VP, _I64, _I64, _I64, _VP, C.c_int32, _I64, _VP, C.c_int32, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
       _VP]),
@@ -335,6 +340,57 @@ def mul_mat_q(*, wtype, weights, ids, y, dst, K, R, n_experts, gate=None, glu_op
                                       nchannels_y * nb, n_used * R, nb, R, ids.stride(0), workspace.data_ptr(),
                                       workspace.numel(), _stream(stream))
     check(rc, "mul_mat_q")
+    return dst
+
+
+def torch_tensor_desc(t, ggml_type: int, name: str = "", keep: list | None = None) -> Tensor:
+    """ggml view of a torch tensor: ne / nb are the reversed shape / byte strides."""
+    d = Tensor()
+    es = t.element_size()
+    ne = list(t.shape)[::-1]
+    nb = [st * es for st in list(t.stride())[::-1]]
+    while len(ne) < 4:                       # trailing dimensions of extent 1, contiguous
+        nb.append(nb[-1] * ne[-1] if nb else es)
+        ne.append(1)
+    d.type = ggml_type
+    d.ne[:] = ne
+    d.nb[:] = nb
+    d.data = t.data_ptr()
+    nm = name.encode()
+    d.name = nm
+    if keep is not None:
+        keep.append(nm)
+    d.has_buffer = 1
+    d.is_view = 0
+    return d
+
+
+GGML_F32, GGML_I32 = 0, 26
+
+
+def mul_mat_id(*, wtype, weights, x, ids, dst, K, R, n_experts, fusion=None, workspace=None, stream=None):
+    """MUL_MAT_ID at the op level through ggml_hip_moe_mul_mat_id.
+
+    weights: device uint8 [n_experts, R, row_bytes]; x: float32 [tokens, channels, K] (rows contiguous);
+    ids: int32 [tokens, >= n_used] (a column slice is a top-k view); dst: float32 [tokens, n_used, R]
+    (any row strides).  Returns dst.
+    """
+    torch = _torch()
+    _require_gpu(weights, x, ids, dst)
+    keep = []
+    src0 = make_tensor(wtype, K, R, n_experts, weights.data_ptr(), keep=keep)
+    s1 = torch_tensor_desc(x, GGML_F32)
+    it = torch_tensor_desc(ids, GGML_I32)
+    dt = torch_tensor_desc(dst, GGML_F32)
+    fp = C.byref(fusion) if fusion is not None else None
+    nbytes = int(lib().ggml_hip_moe_mul_mat_id_workspace_bytes(C.byref(src0), C.byref(s1), C.byref(it), fp))
+    if nbytes < 0:
+        raise MoeError("mul_mat_id: " + lib().ggml_hip_moe_last_error().decode(errors="replace"))
+    if workspace is None or workspace.numel() < nbytes:
+        workspace = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dst.device)
+    rc = lib().ggml_hip_moe_mul_mat_id(C.byref(src0), C.byref(s1), C.byref(it), C.byref(dt), None, fp,
+                                       workspace.data_ptr(), workspace.numel(), _stream(stream))
+    check(rc, "mul_mat_id")
     return dst
 
 

@@ -683,6 +683,71 @@ int quantize_common(int kind, const float *x, void *y, int64_t k, int64_t nrows,
     return 0;
 }
 
+// ---------------------------------------------------------------------------
+// MUL_MAT_ID at the op level: strides from the tensors, path choice, workspace
+// ---------------------------------------------------------------------------
+
+constexpr int GGML_TYPE_F32_ = 0, GGML_TYPE_I32_ = 26;
+constexpr int64_t MMID_GEMV_MAX_TOKENS = 8;   // ggml-cuda's MMVQ batch limit; more tokens take the grouped GEMM
+
+struct MmidPlan {
+    bool cache = false, mmq = false;
+    int64_t K = 0, R = 0, E = 0, n_used = 0, n_tok = 0, ne11 = 0;
+    int kind = 0;                 // activation quantizer: 0 q8_1, 1 q8_K
+    int64_t blk = 32, blk_bytes = 36;
+    uint64_t y_bytes = 0, y_span = 0, ws_mmq = 0;
+};
+
+bool mmq_fusion_ok(const ggml_hip_moe_fusion *f) {
+    return !f || !(f->x_bias || f->gate_bias || f->x_scale || f->gate_scale || f->shared_up);
+}
+
+int mmid_plan(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *src1, const ggml_hip_moe_tensor *ids,
+              const ggml_hip_moe_tensor *dst, const ggml_hip_moe_tensor *gate_host, const ggml_hip_moe_fusion *f,
+              MmidPlan &p) {
+    if (!src0 || !src1 || !ids) return fail(E_INVALID, "mul_mat_id: null tensor");
+    if (!type_supported(src0->type)) return fail(E_UNSUPPORTED, "mul_mat_id: expert type %d is not supported", src0->type);
+    p.K = src0->ne[0];
+    p.R = src0->ne[1];
+    p.E = src0->ne[2];
+    p.n_used = ids->ne[0];
+    p.n_tok = ids->ne[1];
+    p.ne11 = src1->ne[1];
+    if (src0->ne[3] != 1 || src1->ne[3] != 1 || ids->ne[2] != 1 || ids->ne[3] != 1)
+        return fail(E_UNSUPPORTED, "mul_mat_id: 4-d batches are not supported");
+    if (src1->type != GGML_TYPE_F32_ || src1->nb[0] != 4 || src1->ne[0] != p.K || src1->ne[2] != p.n_tok ||
+        p.ne11 < 1 || (src1->nb[1] | src1->nb[2]) & 3 || src1->nb[1] < p.K * 4)
+        return fail(E_INVALID, "mul_mat_id: src1 must be fp32 [K, channels, tokens] with contiguous rows");
+    if (ids->type != GGML_TYPE_I32_ || ids->nb[0] != 4 || ids->nb[1] % 4 || ids->nb[1] < 4 * p.n_used || p.n_used < 1)
+        return fail(E_INVALID, "mul_mat_id: ids must be int32 [n_used, tokens] with contiguous rows");
+    if (dst && (dst->type != GGML_TYPE_F32_ || dst->nb[0] != 4 || dst->ne[0] != p.R || dst->ne[1] != p.n_used ||
+                dst->ne[2] != p.n_tok || (dst->nb[1] | dst->nb[2]) & 3))
+        return fail(E_INVALID, "mul_mat_id: dst must be fp32 [rows, n_used, tokens]");
+    p.cache = wants_impl(src0);
+    const TypeGeom g = type_geom(src0->type);
+    const uint64_t eb = (uint64_t) src0->nb[2];
+    const uintptr_t walign = src0->type == T_Q3_K || src0->type == T_Q6_K ? 1u : src0->type == T_Q2_K ? 3u : 15u;
+    p.mmq = !p.cache && !gate_host && g.kquant && p.n_tok > MMID_GEMV_MAX_TOKENS && mmq_fusion_ok(f) &&
+            p.E <= MMQ_MAX_EXPERTS && p.K % 256 == 0 &&
+            !(((uintptr_t) src0->data | eb | (uintptr_t) (f ? f->gate : nullptr)) & walign) &&
+            !((src0->type == T_Q3_K || src0->type == T_Q6_K) && f && f->gate &&
+              (((uintptr_t) f->gate ^ (uintptr_t) src0->data) & 3u));
+    p.kind = p.mmq ? 1 : 0;
+    p.blk = p.mmq ? 256 : 32;
+    p.blk_bytes = p.mmq ? 292 : 36;
+    if (p.K % p.blk) return fail(E_UNSUPPORTED, "mul_mat_id: K=%lld is not a multiple of %lld", (long long) p.K, (long long) p.blk);
+    p.y_span = (uint64_t) (p.n_tok * p.ne11) * (uint64_t) (p.K / p.blk * p.blk_bytes);
+    p.y_bytes = (p.y_span + 255) & ~(uint64_t) 255;
+    if (p.mmq) {
+        MmqArgs a = {};
+        a.ncols = (int32_t) p.K;
+        a.n_experts = (int32_t) p.E;
+        mmq_layout(a, p.n_tok * p.n_used);
+        p.ws_mmq = a.ws_total;
+    }
+    return 0;
+}
+
 // routing trace files opened by ggml_hip_moe_trace_append: path -> append stream
 std::mutex g_trace_mutex;
 std::unordered_map<std::string, FILE *> g_trace_files;
@@ -971,6 +1036,51 @@ int ggml_hip_moe_mul_mat_q(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_f
     const int rc = dev()->launch_mmq(a, tw, stream);
     if (rc) return dev_err(rc, "mul_mat_q launch");
     return 0;
+}
+
+int64_t ggml_hip_moe_mul_mat_id_workspace_bytes(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *src1,
+                                                const ggml_hip_moe_tensor *ids, const ggml_hip_moe_fusion *fusion) {
+    MmidPlan p;
+    if (mmid_plan(src0, src1, ids, nullptr, nullptr, fusion, p)) return -1;
+    return (int64_t) (p.y_bytes + p.ws_mmq);
+}
+
+int ggml_hip_moe_mul_mat_id(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *src1,
+                            const ggml_hip_moe_tensor *ids, const ggml_hip_moe_tensor *dst,
+                            const ggml_hip_moe_tensor *gate_host, const ggml_hip_moe_fusion *fusion, void *workspace,
+                            int64_t workspace_bytes, void *stream) {
+    if (!dst) return fail(E_INVALID, "mul_mat_id: null dst");
+    MmidPlan p;
+    int rc;
+    if ((rc = mmid_plan(src0, src1, ids, dst, gate_host, fusion, p))) return rc;
+    if (p.n_tok == 0) return 0;
+    if (!workspace || ((uintptr_t) workspace & 255u)) return fail(E_INVALID, "mul_mat_id: workspace must be 256-byte aligned");
+    if ((uint64_t) workspace_bytes < p.y_bytes + p.ws_mmq)
+        return fail(E_INVALID, "mul_mat_id: workspace of %lld bytes, %llu needed", (long long) workspace_bytes,
+                    (unsigned long long) (p.y_bytes + p.ws_mmq));
+    // activations: every (token, channel) row quantized back to back (q8_1 for the GEMV, q8_K for the grouped GEMM)
+    uint8_t *y = (uint8_t *) workspace;
+    const int64_t nb_row = p.K / p.blk;                        // activation blocks per row
+    const float *x = (const float *) src1->data;
+    const int64_t xs1 = src1->nb[1] / 4, xs2 = src1->nb[2] / 4;
+    if (xs2 == xs1 * p.ne11) {
+        if ((rc = quantize_common(p.kind, x, y, p.K, p.ne11 * p.n_tok, xs1, nb_row, stream))) return rc;
+    } else {
+        for (int64_t t = 0; t < p.n_tok; ++t)
+            if ((rc = quantize_common(p.kind, x + t * xs2, y + t * p.ne11 * nb_row * p.blk_bytes, p.K, p.ne11, xs1, nb_row,
+                                      stream)))
+                return rc;
+    }
+    const int64_t ids_stride = ids->nb[1] / 4;
+    const int64_t sc_dst = dst->nb[2] / 4, sch_dst = dst->nb[1] / 4;
+    if (p.mmq) {
+        return ggml_hip_moe_mul_mat_q(src0, fusion, y, (const int32_t *) ids->data, (float *) dst->data,
+                                      p.K, p.R, p.E, p.n_tok, p.ne11, p.n_used, p.ne11 * nb_row, sc_dst, nb_row, sch_dst,
+                                      ids_stride, y + p.y_bytes, (int64_t) p.ws_mmq, stream);
+    }
+    return gemv_common(p.cache ? 1 : 0, ACT_Q8_1, src0, gate_host, fusion, y, (const int32_t *) ids->data,
+                       (float *) dst->data, p.K, p.R, p.E, p.n_tok, p.ne11, p.n_used, p.ne11 * nb_row, sc_dst, nb_row,
+                       sch_dst, ids_stride, stream);
 }
 
 int ggml_hip_ssm_conv_f32(const float *src0, int64_t src0_nb0, int64_t src0_nb1, int64_t src0_nb2, const void *src1,

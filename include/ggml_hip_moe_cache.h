@@ -351,6 +351,39 @@ int ggml_hip_moe_cache_totals(ggml_hip_moe_totals *out);
 int ggml_hip_moe_cache_reset(void);
 
 /* ---------------------------------------------------------------------
+ * MUL_MAT_ID at the ggml op level: the caller side of the reference's
+ * intercept (patches/apply_patches.py:42-62 / results/final.patch:66-82, where
+ * ggml-cuda has already derived the strides and quantized src1), as one call
+ * that takes the op's tensors.
+ *
+ *   src0  expert weights [K, R, E] (any supported type; host-resident tensors
+ *         take the pointer-table cache path when ggml_hip_moe_cache_wants(src0))
+ *   src1  fp32 activations [K, channels, tokens] (channels 1: every slot reads
+ *         the token's row; n_used: one row per slot), rows contiguous
+ *   ids   int32 [n_used, tokens], any row stride (a top-k view)
+ *   dst   fp32 [R, n_used, tokens], any row strides
+ *
+ * Strides are derived from ne/nb as ggml-cuda does (ids_stride = ids->nb[1]/4,
+ * stride_channel_dst = dst->nb[1]/4, stride_col_dst = dst->nb[2]/4); src1 is
+ * quantized into `workspace` (q8_1 rows for the GEMV, q8_K rows for the grouped
+ * GEMM) and the op runs on `stream`:
+ *   - the pointer-table cache GEMV when the cache wants src0;
+ *   - the expert-grouped int8-MFMA GEMM (ggml_hip_moe_mul_mat_q) for K-quant
+ *     experts with more than 8 tokens (ggml-cuda's MMVQ batch limit) when the
+ *     fusion is at most gate + GLU and the weights are aligned for it;
+ *   - the device-resident GEMV otherwise.
+ * gate_host / fusion as in ggml_hip_moe_cache_mul_mat_vec_q.  The workspace (256-
+ * byte aligned) must hold ggml_hip_moe_mul_mat_id_workspace_bytes(...) bytes
+ * (-1: the tensors are not a supported MUL_MAT_ID).
+ * --------------------------------------------------------------------- */
+int64_t ggml_hip_moe_mul_mat_id_workspace_bytes(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *src1,
+                                                const ggml_hip_moe_tensor *ids, const ggml_hip_moe_fusion *fusion);
+int ggml_hip_moe_mul_mat_id(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *src1,
+                            const ggml_hip_moe_tensor *ids, const ggml_hip_moe_tensor *dst,
+                            const ggml_hip_moe_tensor *gate_host, const ggml_hip_moe_fusion *fusion,
+                            void *workspace, int64_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------
  * SSM_CONV with F32 or F16 conv weights (kernels/ssm-conv.cu:117-217: the
  * reference's ssm_conv_f32_cuda / ggml_cuda_op_ssm_conv, templated on the
  * weight type so that F16 conv1d weights work; the fused ADD(bias) + SiLU).
