@@ -128,16 +128,33 @@ def load_traffic(fused):
         return None
 
 
-def cpu_baseline(torch, model, ids, w, budget_s=12.0):
-    """ggml-CPU MUL_MAT_ID restatement (oracle) over layer 0's weights, on this host's cores."""
-    import numpy as np
+def cpu_baseline(torch, model, ids, w, budget_s=12.0, budget_1t_s=6.0):
+    """ggml-CPU MUL_MAT_ID restatement (oracle) over layer 0's weights, on this host's cores
+    (all of them, then one thread)."""
     sys.path.insert(0, str(ROOT))
     from oracle import oracle as O
     nth = int(os.environ.get("OMP_NUM_THREADS", "0")) or O.cpu_cores()
     ly = model.layers[0]
+    mats = tuple(t.cpu().numpy() for t in (ly.gate, ly.up, ly.down, ly.sh_gate, ly.sh_up, ly.sh_down))
+    layer_bytes = model.bytes_per_token() / model.L
+    n, el = _cpu_layer_loop(O, model, mats, ids, w, nth, budget_s)
+    n1, el1 = _cpu_layer_loop(O, model, mats, ids, w, 1, budget_1t_s)
+    return {"value": round(n * layer_bytes / el / 1e9, 3), "unit": "GB/s", "cores": nth, "kind": "port",
+            "sample": f"{n} layer-tokens of the same MoE layer (512 experts Q2_K gate/up/down + Q4_K shared, "
+                      f"B=1, fresh top-8 routing each) through the oracle's ggml-CPU MUL_MAT_ID restatement "
+                      f"(q8_K activations, scalar vec_dot, OpenMP rows), GLU/combine unfused; {el:.1f} s",
+            "layer_tok_per_s": round(n / el, 3),
+            "one_thread": {"value": round(n1 * layer_bytes / el1 / 1e9, 3), "unit": "GB/s", "cores": 1,
+                           "layer_tok_per_s": round(n1 / el1, 3),
+                           "sample": f"{n1} layer-tokens of the same layer and routing stream; {el1:.1f} s"}}
+
+
+def _cpu_layer_loop(O, model, mats, ids, w, nth, budget_s):
+    """Layer-tokens through the CPU restatement on nth threads until budget_s has passed:
+    returns (layer-tokens, seconds)."""
+    import numpy as np
+    gate, up, down, sg, su, sd = mats
     H, F, U, E = model.H, model.F, model.U, model.E
-    gate, up, down = ly.gate.cpu().numpy(), ly.up.cpu().numpy(), ly.down.cpu().numpy()
-    sg, su, sd = ly.sh_gate.cpu().numpy(), ly.sh_up.cpu().numpy(), ly.sh_down.cpu().numpy()
     x = np.random.default_rng(1).standard_normal((1, H)).astype(np.float32)
     t0 = time.perf_counter()
     n = 0
@@ -158,12 +175,7 @@ def cpu_baseline(torch, model, ids, w, budget_s=12.0):
         el = time.perf_counter() - t0
         if el >= budget_s:
             break
-    layer_bytes = model.bytes_per_token() / model.L
-    return {"value": round(n * layer_bytes / el / 1e9, 3), "unit": "GB/s", "cores": nth, "kind": "port",
-            "sample": f"{n} layer-tokens of the same MoE layer (512 experts Q2_K gate/up/down + Q4_K shared, "
-                      f"B=1, fresh top-8 routing each) through the oracle's ggml-CPU MUL_MAT_ID restatement "
-                      f"(q8_K activations, scalar vec_dot, OpenMP rows), GLU/combine unfused; {el:.1f} s",
-            "layer_tok_per_s": round(n / el, 3)}
+    return n, el
 
 
 def main():
@@ -248,7 +260,8 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(torch, model, ids_np, w_np)
-        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads")
+        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads, "
+            f"{cpu['one_thread']['value']} GB/s on 1 thread")
 
     out = {
         "metric": METRIC,
