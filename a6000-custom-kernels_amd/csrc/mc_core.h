@@ -9,6 +9,14 @@
 
 #include "mc_internal.h"
 
+// Cache-policy bits of the decode GEMV's weight DMA (buffer->LDS loads).  Each span
+// is contiguous and read once per launch, so it goes out non-temporal (nt, bit 1):
+// the stream then does not push the activation rows, ids and tables, which every
+// workgroup reads, out of L2.
+#ifndef MC_WEIGHT_CPOL
+#define MC_WEIGHT_CPOL 2
+#endif
+
 namespace mc {
 
 typedef uint32_t u32;
@@ -531,18 +539,18 @@ __device__ __forceinline__ int dma_span(const uint8_t *base, u32 base_bytes, u32
 #pragma unroll
         for (int i = 0; i < MAXR; ++i) {
             if (i < rounds) {
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * i), 16, lane_off + 1024u * i, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * i), 16, lane_off + 1024u * i, 0, 0, MC_WEIGHT_CPOL);
             }
         }
     } else {
 #pragma unroll
         for (int i = 0; i < MAXR; ++i) {
             if (i < rounds - 1)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * i), 16, lane_off + 1024u * i, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * i), 16, lane_off + 1024u * i, 0, 0, MC_WEIGHT_CPOL);
         }
         const u32 last = (u32) (rounds - 1);
         if (16u * (threadIdx.x % WAVE) < lead + nbytes - 1024u * last)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * last), 16, lane_off + 1024u * last, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * last), 16, lane_off + 1024u * last, 0, 0, MC_WEIGHT_CPOL);
     }
     return rounds;
 }
