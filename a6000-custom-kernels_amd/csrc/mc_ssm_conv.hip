@@ -55,7 +55,9 @@ __global__ __launch_bounds__(SSM_WAVES * WAVE) void mc_ssm_conv_kernel(const Ssm
         const int row = i / P, col = i % P;
         v[k] = 0.0f;
         if (i < N_EL && row < n_ch && col < n_cols)
-            v[k] = ((const float *) (xs + (int64_t) (r0 + row) * a.x_nb1))[t0 + col];
+            // non-temporal: the input is read once per tile, while the taps and bias,
+            // which every tile reads, stay in L2
+            v[k] = __builtin_nontemporal_load(((const float *) (xs + (int64_t) (r0 + row) * a.x_nb1)) + t0 + col);
     }
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
