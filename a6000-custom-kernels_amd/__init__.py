@@ -122,6 +122,8 @@ SIGNATURES = [
       _VP]),
     ("ggml_hip_moe_trace_append", C.c_int, [C.c_char_p, C.c_char_p, C.c_void_p, _I64, _I64, _I64]),
     ("ggml_hip_moe_trace_close", C.c_int, []),
+    ("ggml_hip_moe_check_status", C.c_int, [_VP]),
+    ("ggml_hip_moe_debug_set_spin_limit", C.c_int, [_I64]),
     ("ggml_hip_moe_last_error", C.c_char_p, []),
     ("ggml_hip_moe_version", C.c_char_p, []),
 ]
@@ -151,6 +153,9 @@ def lib() -> C.CDLL:
                            "(or __graft_entry__.build()); there is no CPU fallback")
         _lib = bind(LIB_PATH)
     return _lib
+
+
+E_INVALID, E_UNSUPPORTED, E_DEVICE, E_DISABLED, E_STATE, E_TIMEOUT = -1, -2, -3, -4, -5, -6
 
 
 def check(rc: int, what: str = "") -> int:
@@ -429,6 +434,11 @@ def configure(*, enabled=True, slots=-1, budget_gb=0.0, margin_gb=2.0, seed_path
     cfg.seed_path = cfg._seed
     cfg.max_promotions, cfg.verbose = max_promotions, int(verbose)
     check(lib().ggml_hip_moe_cache_configure(C.byref(cfg)), "configure")
+
+
+def check_status(stream=None) -> int:
+    """0, or E_TIMEOUT when a fused gate/up launch on `stream` had a bounded wait give up (then cleared)."""
+    return lib().ggml_hip_moe_check_status(_stream(stream))
 
 
 def reset():

@@ -14,7 +14,7 @@
 
 namespace mc {
 
-enum PtrKind : int { PTR_ERROR = -1, PTR_UNREGISTERED = 0, PTR_HOST = 1, PTR_DEVICE = 2 };
+enum PtrKind : int { PTR_ERROR = -1, PTR_UNREGISTERED = 0, PTR_HOST = 1, PTR_DEVICE = 2, PTR_MANAGED = 3 };
 
 struct Device {
     virtual ~Device() = default;
@@ -36,6 +36,7 @@ struct Device {
     virtual int launch_combine(const CombineArgs &c, void *stream) = 0;
     virtual int launch_mmq(const MmqArgs &m, int type, void *stream) = 0;
     virtual int launch_ssm_conv(const SsmConvArgs &a, void *stream) = 0;
+    virtual int status_address(uint32_t **p) = 0;                          // device status word of the current device
     virtual const char *error_string(int code) = 0;
 };
 

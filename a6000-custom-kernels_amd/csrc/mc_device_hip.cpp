@@ -10,6 +10,7 @@ int launch_quantize(int kind, const QuantArgs &q, void *stream);      // mc_kern
 int launch_combine(const CombineArgs &c, void *stream);               // mc_kernels.hip
 int launch_mmq(const MmqArgs &m, int type, void *stream);            // mc_mmq.hip
 int launch_ssm_conv(const SsmConvArgs &a, void *stream);              // mc_ssm_conv.hip
+int status_address(uint32_t **p);                                     // mc_ffn.hip
 
 namespace {
 
@@ -37,7 +38,9 @@ struct HipDevice final : Device {
             (void) hipGetLastError();   // an unregistered pointer is not an error state
             return PTR_UNREGISTERED;
         }
-        if (attr.type == hipMemoryTypeHost || attr.type == hipMemoryTypeManaged) return PTR_HOST;
+        // only host memory qualifies for the cache (kernels/moe-cache.cu:437 accepts cudaMemoryTypeHost alone)
+        if (attr.type == hipMemoryTypeHost) return PTR_HOST;
+        if (attr.type == hipMemoryTypeManaged) return PTR_MANAGED;
         if (attr.type == hipMemoryTypeDevice) return PTR_DEVICE;
         return PTR_UNREGISTERED;
     }
@@ -56,6 +59,7 @@ struct HipDevice final : Device {
     int launch_combine(const CombineArgs &c, void *s) override { return mc::launch_combine(c, s); }
     int launch_mmq(const MmqArgs &m, int type, void *s) override { return mc::launch_mmq(m, type, s); }
     int launch_ssm_conv(const SsmConvArgs &a, void *s) override { return mc::launch_ssm_conv(a, s); }
+    int status_address(uint32_t **p) override { return mc::status_address(p); }
     const char *error_string(int code) override { return hipGetErrorString((hipError_t) code); }
 };
 

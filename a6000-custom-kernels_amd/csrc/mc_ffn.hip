@@ -32,6 +32,8 @@
 // counters instead of a barrier.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "mc_core.h"
 #include "mc_internal.h"
 #include "mc_step.h"
@@ -39,16 +41,52 @@
 namespace mc {
 
 // ---------------------------------------------------------------------------
+// device status word
+// ---------------------------------------------------------------------------
+
+// STATUS_* bits set by a kernel that could not finish its work (a bounded wait
+// that gave up).  One word per GPU for the life of the process.  Host code never
+// passes this name to a kernel: it uses the address hipGetSymbolAddress returns
+// with that GPU current (status_address), which differs from GPU to GPU.
+static __device__ __align__(256) u32 status_word[64];
+
+constexpr int MAX_DEVICES = 64;
+
+// Device address of the current GPU's status word (looked up once per GPU).
+int status_address(u32 **out) {
+    static std::mutex m;
+    static u32 *addr[MAX_DEVICES] = {};
+    int d = 0;
+    hipError_t err = hipGetDevice(&d);
+    if (err != hipSuccess) return (int) err;
+    if (d < 0 || d >= MAX_DEVICES) return (int) hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(m);
+    if (!addr[d]) {
+        void *p = nullptr;
+        err = hipGetSymbolAddress(&p, HIP_SYMBOL(status_word));
+        if (err != hipSuccess) return (int) err;
+        addr[d] = (u32 *) p;
+    }
+    *out = addr[d];
+    return (int) hipSuccess;
+}
+
+// ---------------------------------------------------------------------------
 // gate/up with the RMSNorm + q8_1 prologue
 // ---------------------------------------------------------------------------
 
-// Waits (bounded) until the LDS counter reaches n; false on timeout.  The LDS reads
-// a wave issues afterwards are ordered after this read by the LDS unit.
-__device__ __forceinline__ bool wait_lds_count(const u32 *cnt, u32 n) {
-    for (int it = 0; it < (1 << 22); ++it) {
+// Waits (bounded: a.spin_limit polls) until the LDS counter reaches n.  On timeout it
+// sets STATUS_WAIT_TIMEOUT in the status word (the host reads it with
+// ggml_hip_moe_check_status) and returns false; the caller then skips the work that
+// needed the count and still exits.  The LDS reads a wave issues afterwards are
+// ordered after this read by the LDS unit.
+__device__ __forceinline__ bool wait_lds_count(const GemvArgs &a, const u32 *cnt, u32 n) {
+    for (int it = 0; it < a.spin_limit; ++it) {
         if (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= n) return true;
         __builtin_amdgcn_s_sleep(1);
     }
+    if (threadIdx.x % WAVE == 0)
+        __hip_atomic_fetch_or(a.status, STATUS_WAIT_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return false;
 }
 
@@ -84,7 +122,7 @@ __device__ __forceinline__ void gu_prologue(const GemvArgs &a, int t, int p, flo
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");      // the sums are in LDS before the count
     if (lane == 0) __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    wait_lds_count(sync, (u32) NP);
+    wait_lds_count(a, sync, (u32) NP);            // on timeout the row is wrong and the status word says so
     float ss = 0.0f;                                          // ascending, as every other producer of y
 #pragma unroll
     for (int j = 0; j < NP * PC; ++j)
@@ -189,14 +227,14 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
         run = s.valid;
     }
     if (run) {
-        wait_lds_count(sync + 2, (u32) NP);                   // the prologue's loads go out first
+        wait_lds_count(a, sync + 2, (u32) NP);                // the prologue's loads go out first
         if (sh) {
             if constexpr (TS != 0) step_dma<TS, true>(a, s, span);
         } else {
             step_dma<TW, true>(a, s, span);
         }
         wait_loads_at_most(s.wgate ? s.n_up : 0);             // gate span landed (up may still land)
-        run = wait_lds_count(sync + 1, (u32) NP);             // the normalized row is complete
+        run = wait_lds_count(a, sync + 1, (u32) NP);          // the normalized row is complete
     }
     float v = 0.0f;
     int rl = -1;
@@ -213,6 +251,7 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
         }
     }
     if (a.hq) gu_block_q8_1(a, t, local0, sw, sh ? a.sh_rps : a.rps, run, rl, v, red + 32, sync + 3);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");      // a step skipped after a timeout: its DMA has landed
 }
 
 // ---------------------------------------------------------------------------

@@ -45,6 +45,9 @@ constexpr int E_UNSUPPORTED = -2;
 constexpr int E_DEVICE = -3;
 constexpr int E_DISABLED = -4;
 constexpr int E_STATE = -5;
+constexpr int E_TIMEOUT = -6;
+
+int32_t g_spin_limit = DEFAULT_SPIN_LIMIT;             // bounded in-kernel waits (debug setter below)
 
 // ---------------------------------------------------------------------------
 // configuration (kernels/moe-cache.cu:330-363)
@@ -257,29 +260,24 @@ int get_or_create_locked(const ggml_hip_moe_tensor *src0, void *stream, Entry **
     if (slots > e->n_experts) slots = e->n_experts;
     e->n_slots = (int) slots;
 
+    // Any failure below frees what this registration allocated and registers nothing, so
+    // a later call never finds an entry whose device table was not written.
+    auto abandon = [&](int code, const char *what) {
+        if (e->pool) dev()->free_dev(e->pool);
+        if (e->d_stamps) dev()->free_dev(e->d_stamps);
+        if (e->d_tbl) dev()->free_dev(e->d_tbl);
+        delete e;
+        return dev_err(code, what);
+    };
     e->h_tbl.resize(e->n_experts);
     for (int i = 0; i < e->n_experts; ++i) e->h_tbl[i] = host_entry(e, i);
-    if ((rc = dev()->malloc_dev((void **) &e->d_tbl, sizeof(uint64_t) * e->n_experts))) { delete e; return dev_err(rc, "table alloc"); }
-    if ((rc = dev()->malloc_dev((void **) &e->d_stamps, sizeof(uint32_t) * e->n_experts))) {
-        dev()->free_dev(e->d_tbl);
-        delete e;
-        return dev_err(rc, "stamps alloc");
-    }
-    if ((rc = dev()->memset_dev(e->d_stamps, 0, sizeof(uint32_t) * e->n_experts, stream))) return dev_err(rc, "stamps clear");
+    if ((rc = dev()->malloc_dev((void **) &e->d_tbl, sizeof(uint64_t) * e->n_experts))) return abandon(rc, "table alloc");
+    if ((rc = dev()->malloc_dev((void **) &e->d_stamps, sizeof(uint32_t) * e->n_experts))) return abandon(rc, "stamps alloc");
+    if ((rc = dev()->memset_dev(e->d_stamps, 0, sizeof(uint32_t) * e->n_experts, stream))) return abandon(rc, "stamps clear");
     e->h_stamps.assign(e->n_experts, 0);
     e->slot_of.assign(e->n_experts, -1);
     e->expert_of.assign(e->n_slots, -1);
-    if (e->n_slots > 0) {
-        if ((rc = dev()->malloc_dev((void **) &e->pool, (size_t) e->n_slots * eb))) {
-            dev()->free_dev(e->d_tbl);
-            dev()->free_dev(e->d_stamps);
-            delete e;
-            return dev_err(rc, "pool alloc");
-        }
-        g_used += (size_t) e->n_slots * eb;
-    }
-    g_by_data[e->data] = e;
-    g_all.push_back(e);
+    if (e->n_slots > 0 && (rc = dev()->malloc_dev((void **) &e->pool, (size_t) e->n_slots * eb))) return abandon(rc, "pool alloc");
 
     // seed slots 0..k-1 in seed order, skipping out-of-range and repeated ids
     load_seed_locked();
@@ -291,7 +289,7 @@ int get_or_create_locked(const ggml_hip_moe_tensor *src0, void *stream, Entry **
             if (expert < 0 || expert >= e->n_experts || e->slot_of[expert] >= 0) continue;
             const int slot = seeded;
             if ((rc = dev()->copy_h2d(e->pool + (size_t) slot * eb, e->data + (size_t) expert * eb, eb, stream)))
-                return dev_err(rc, "seed copy");
+                return abandon(rc, "seed copy");
             e->h_tbl[expert] = pool_entry(e, slot);
             e->slot_of[expert] = slot;
             e->expert_of[slot] = expert;
@@ -300,7 +298,10 @@ int get_or_create_locked(const ggml_hip_moe_tensor *src0, void *stream, Entry **
     }
     // one upload covers the host entries and every seeded slot, ordered after the copies
     if ((rc = dev()->copy_h2d(e->d_tbl, e->h_tbl.data(), sizeof(uint64_t) * e->n_experts, stream)))
-        return dev_err(rc, "table upload");
+        return abandon(rc, "table upload");
+    if (e->n_slots > 0) g_used += (size_t) e->n_slots * eb;
+    g_by_data[e->data] = e;
+    g_all.push_back(e);
     if (g_cfg.verbose) {
         fprintf(stderr, "moe-cache: registered %s type=%d experts=%d slot_bytes=%zu slots=%d seeded=%d (pool %.1f MB, total %.2f GB, free HBM %.2f GB)\n",
                 e->name.empty() ? "<tensor>" : e->name.c_str(), e->type, e->n_experts, eb, e->n_slots, seeded,
@@ -504,7 +505,7 @@ int gemv_common(int use_cache, int act, const ggml_hip_moe_tensor *src0, const g
                 const ggml_hip_moe_fusion *fusion, const void *src1, const int32_t *ids_d, float *dst_d,
                 int64_t ne00, int64_t ne01, int64_t ne02, int64_t ncols_dst, int64_t nchannels_y, int64_t nchannels_dst,
                 int64_t stride_col_y, int64_t stride_col_dst, int64_t stride_channel_y, int64_t stride_channel_dst,
-                int64_t ids_stride, void *stream, const FfnExtra *fx = nullptr) {
+                int64_t ids_stride, void *stream, const FfnExtra *fx = nullptr, bool no_tables = false) {
     const int mode = fx ? fx->mode : FFN_NONE;
     if (!src0 || !src1 || !ids_d || !dst_d) return fail(E_INVALID, "moe-gemv: null argument");
     const int tw = src0->type;
@@ -571,6 +572,7 @@ int gemv_common(int use_cache, int act, const ggml_hip_moe_tensor *src0, const g
     a.cache_id_gate = -1;
     a.glu_op = 2;                  // SWIGLU unless the fusion says otherwise (kernels/moe-cache.cu:116)
     a.bias_stride = stride_channel_dst;
+    a.spin_limit = __atomic_load_n(&g_spin_limit, __ATOMIC_RELAXED);
     if (fusion) {
         a.x_bias = fusion->x_bias;
         a.gate_bias = fusion->gate_bias;
@@ -625,15 +627,19 @@ int gemv_common(int use_cache, int act, const ggml_hip_moe_tensor *src0, const g
             }
             a.has_gate = 1;
         }
-    } else {
+    } else if (!no_tables) {
         Resident *r;
         if ((rc = resident_table_locked(src0->data, (int) ne02, eb, stream, &r))) return rc;
         a.tbl = r->d_tbl;
     }
     if (fusion && fusion->gate) {
-        Resident *r;
-        if ((rc = resident_table_locked(fusion->gate, (int) ne02, eb, stream, &r))) return rc;
-        a.tbl_gate = r->d_tbl;
+        // device-resident experts are addressed affinely (w_base below); the table only serves
+        // the cache path, whose up tensor goes through a table too
+        if (!no_tables) {
+            Resident *r;
+            if ((rc = resident_table_locked(fusion->gate, (int) ne02, eb, stream, &r))) return rc;
+            a.tbl_gate = r->d_tbl;
+        }
         a.has_gate = 1;
     }
     if (!use_cache) {
@@ -660,6 +666,7 @@ int gemv_common(int use_cache, int act, const ggml_hip_moe_tensor *src0, const g
         a.x_out = fx->x_out;
         a.x_stride = fx->x_stride;
     }
+    if ((rc = dev()->status_address(&a.status))) return dev_err(rc, "status word lookup");
     if ((rc = dev()->launch_gemv(a, tw, ts, act, stream))) return dev_err(rc, mode == FFN_NONE ? "GEMV launch" : "fused FFN launch");
     return 0;
 }
@@ -746,6 +753,38 @@ int mmid_plan(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *src1, 
         p.ws_mmq = a.ws_total;
     }
     return 0;
+}
+
+
+// The op-level MUL_MAT_ID once planned: src1 quantized into the workspace, then the
+// grouped GEMM or the GEMV (no_tables: device-resident experts addressed affinely,
+// no resident pointer table is built, so nothing is allocated).
+int mmid_run(const MmidPlan &p, const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *src1,
+             const ggml_hip_moe_tensor *ids, const ggml_hip_moe_tensor *dst, const ggml_hip_moe_tensor *gate_host,
+             const ggml_hip_moe_fusion *fusion, uint8_t *y, void *stream, bool no_tables) {
+    int rc;
+    // activations: every (token, channel) row quantized back to back (q8_1 for the GEMV, q8_K for the grouped GEMM)
+    const int64_t nb_row = p.K / p.blk;                        // activation blocks per row
+    const float *x = (const float *) src1->data;
+    const int64_t xs1 = src1->nb[1] / 4, xs2 = src1->nb[2] / 4;
+    if (xs2 == xs1 * p.ne11) {
+        if ((rc = quantize_common(p.kind, x, y, p.K, p.ne11 * p.n_tok, xs1, nb_row, stream))) return rc;
+    } else {
+        for (int64_t t = 0; t < p.n_tok; ++t)
+            if ((rc = quantize_common(p.kind, x + t * xs2, y + t * p.ne11 * nb_row * p.blk_bytes, p.K, p.ne11, xs1, nb_row,
+                                      stream)))
+                return rc;
+    }
+    const int64_t ids_stride = ids->nb[1] / 4;
+    const int64_t sc_dst = dst->nb[2] / 4, sch_dst = dst->nb[1] / 4;
+    if (p.mmq) {
+        return ggml_hip_moe_mul_mat_q(src0, fusion, y, (const int32_t *) ids->data, (float *) dst->data,
+                                      p.K, p.R, p.E, p.n_tok, p.ne11, p.n_used, p.ne11 * nb_row, sc_dst, nb_row, sch_dst,
+                                      ids_stride, y + p.y_bytes, (int64_t) p.ws_mmq, stream);
+    }
+    return gemv_common(p.cache ? 1 : 0, ACT_Q8_1, src0, gate_host, fusion, y, (const int32_t *) ids->data,
+                       (float *) dst->data, p.K, p.R, p.E, p.n_tok, p.ne11, p.n_used, p.ne11 * nb_row, sc_dst, nb_row,
+                       sch_dst, ids_stride, stream, nullptr, no_tables);
 }
 
 // routing trace files opened by ggml_hip_moe_trace_append: path -> append stream
@@ -899,7 +938,7 @@ int ggml_hip_moe_cache_pin_host(const ggml_hip_moe_tensor *t) {
     if (!t || !t->has_buffer || !t->data) return 0;
     const int kind = dev()->ptr_kind(t->data);
     if (kind == PTR_HOST) return 1;
-    if (kind == PTR_DEVICE || kind == PTR_ERROR) return 0;
+    if (kind == PTR_DEVICE || kind == PTR_MANAGED || kind == PTR_ERROR) return 0;
     if (!g_cfg.allow_register) {
         fail(E_STATE, "moe-cache: %s is not GPU-readable; allocate it with hipHostMalloc or set GGML_HIP_MOE_CACHE_ALLOW_REGISTER=1",
              t->name ? t->name : "<tensor>");
@@ -1058,29 +1097,7 @@ int ggml_hip_moe_mul_mat_id(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_
     if ((uint64_t) workspace_bytes < p.y_bytes + p.ws_mmq)
         return fail(E_INVALID, "mul_mat_id: workspace of %lld bytes, %llu needed", (long long) workspace_bytes,
                     (unsigned long long) (p.y_bytes + p.ws_mmq));
-    // activations: every (token, channel) row quantized back to back (q8_1 for the GEMV, q8_K for the grouped GEMM)
-    uint8_t *y = (uint8_t *) workspace;
-    const int64_t nb_row = p.K / p.blk;                        // activation blocks per row
-    const float *x = (const float *) src1->data;
-    const int64_t xs1 = src1->nb[1] / 4, xs2 = src1->nb[2] / 4;
-    if (xs2 == xs1 * p.ne11) {
-        if ((rc = quantize_common(p.kind, x, y, p.K, p.ne11 * p.n_tok, xs1, nb_row, stream))) return rc;
-    } else {
-        for (int64_t t = 0; t < p.n_tok; ++t)
-            if ((rc = quantize_common(p.kind, x + t * xs2, y + t * p.ne11 * nb_row * p.blk_bytes, p.K, p.ne11, xs1, nb_row,
-                                      stream)))
-                return rc;
-    }
-    const int64_t ids_stride = ids->nb[1] / 4;
-    const int64_t sc_dst = dst->nb[2] / 4, sch_dst = dst->nb[1] / 4;
-    if (p.mmq) {
-        return ggml_hip_moe_mul_mat_q(src0, fusion, y, (const int32_t *) ids->data, (float *) dst->data,
-                                      p.K, p.R, p.E, p.n_tok, p.ne11, p.n_used, p.ne11 * nb_row, sc_dst, nb_row, sch_dst,
-                                      ids_stride, y + p.y_bytes, (int64_t) p.ws_mmq, stream);
-    }
-    return gemv_common(p.cache ? 1 : 0, ACT_Q8_1, src0, gate_host, fusion, y, (const int32_t *) ids->data,
-                       (float *) dst->data, p.K, p.R, p.E, p.n_tok, p.ne11, p.n_used, p.ne11 * nb_row, sc_dst, nb_row,
-                       sch_dst, ids_stride, stream);
+    return mmid_run(p, src0, src1, ids, dst, gate_host, fusion, (uint8_t *) workspace, stream, false);
 }
 
 int ggml_hip_ssm_conv_f32(const float *src0, int64_t src0_nb0, int64_t src0_nb1, int64_t src0_nb2, const void *src1,
@@ -1335,6 +1352,32 @@ int ggml_hip_moe_trace_close(void) {
         if (kv.second && fclose(kv.second) != 0 && !rc) rc = fail(E_INVALID, "trace_close: %s", kv.first.c_str());
     g_trace_files.clear();
     return rc;
+}
+
+int ggml_hip_moe_check_status(void *stream) {
+    uint32_t *status = nullptr;
+    int rc;
+    if ((rc = dev()->status_address(&status))) return dev_err(rc, "status word lookup");
+    uint32_t *h = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_mutex);
+        if ((rc = init_globals_locked(stream))) return rc;
+        h = &g_h_stats[STATS_WORDS + 1];                  // pinned staging word
+        if ((rc = dev()->copy_d2h(h, status, sizeof(uint32_t), stream))) return dev_err(rc, "status readback");
+        if ((rc = dev()->sync(stream))) return dev_err(rc, "stream sync");
+        const uint32_t v = *h;
+        if (v == 0) return 0;
+        if ((rc = dev()->memset_dev(status, 0, sizeof(uint32_t), stream))) return dev_err(rc, "status clear");
+        if ((rc = dev()->sync(stream))) return dev_err(rc, "stream sync");
+        return fail(E_TIMEOUT, "moe-ffn: a bounded in-kernel wait gave up (status 0x%x): the outputs of the fused "
+                    "gate/up launches since the last check are not valid", v);
+    }
+}
+
+int ggml_hip_moe_debug_set_spin_limit(int64_t n) {
+    const int32_t v = n < 0 ? DEFAULT_SPIN_LIMIT : (int32_t) std::min<int64_t>(n, INT32_MAX);
+    __atomic_store_n(&g_spin_limit, v, __ATOMIC_RELAXED);
+    return 0;
 }
 
 const char *ggml_hip_moe_last_error(void) { return t_last_error.c_str(); }

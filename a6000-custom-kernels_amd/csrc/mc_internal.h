@@ -154,7 +154,14 @@ struct GemvArgs {
     const float *residual;        // [n_tok][x_stride], or null
     float *x_out;                 // [n_tok][x_stride]
     int64_t x_stride;             // floats
+    // device status word (STATUS_* bits), set by a kernel that could not finish its work
+    uint32_t *status;
+    int32_t spin_limit;           // iterations of a bounded in-kernel wait before it gives up
 };
+
+// Device status bits (ggml_hip_moe_check_status).
+constexpr uint32_t STATUS_WAIT_TIMEOUT = 1u;   // a bounded wait of the fused gate/up kernel gave up
+constexpr int32_t DEFAULT_SPIN_LIMIT = 1 << 22;
 
 enum : int { FFN_NONE = 0, FFN_GATE_UP_NORM = 1, FFN_DOWN_COMBINE = 2 };
 constexpr int FFN_GU_MAX_WAVES = 8;    // gate/up workgroups: up to 8 step waves sharing one normalized row

@@ -28,10 +28,15 @@ namespace mc {
 // One wave.  Miss-log entries are written at canonical positions (pick order,
 // token-major, up before gate): one legal ordering of the reference's
 // atomicAdd-ordered log; the multiset and the counters are the reference's.
+// The gate is recorded only when it has a cache entry of its own
+// (cache_id_gate >= 0): a device-resident gate reached through a resident
+// table for addressing leaves no stamp, hit or miss, as the reference's null
+// tbl_gate does (kernels/moe-cache.cu:178-201, :804).
 static __device__ void record_picks(const GemvArgs &a) {
     const int lane = threadIdx.x % WAVE;
     const int n_picks = a.n_tok * a.n_used;
     const u32 clk = a.clock ? *a.clock : 0u;
+    const bool rec_gate = a.tbl_gate && a.cache_id_gate >= 0;
     for (int p0 = 0; p0 < n_picks; p0 += WAVE) {
         const int p = p0 + lane;
         int e = -1;
@@ -44,7 +49,7 @@ static __device__ void record_picks(const GemvArgs &a) {
                 if (a.stamps) a.stamps[e] = clk;
                 miss_up = (u32) (pu & 1u);
                 hits += 1u - miss_up;
-                if (a.tbl_gate) {
+                if (rec_gate) {
                     const uint64_t pg = a.tbl_gate[e];
                     if (a.stamps_gate) a.stamps_gate[e] = clk;
                     miss_gate = (u32) (pg & 1u);

@@ -9,8 +9,8 @@
  * every function returns a status instead of aborting (the reference aborts
  * through CUDA_CHECK / GGML_ABORT: kernels/moe-cache.cu:475-480, 864).
  *
- * Status codes: 0 = success, < 0 = error (text in ggml_hip_moe_last_error()).
- * Boolean predicates return 1 / 0.
+ * Status codes: 0 = success, < 0 = error (GGML_HIP_MOE_E_*, text in
+ * ggml_hip_moe_last_error()).  Boolean predicates return 1 / 0.
  *
  * Ownership (kernels/moe-cache.cu:568-581): the library owns the pool, the
  * pointer tables, the stamp arrays and the global stats/clock it allocates;
@@ -33,6 +33,17 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+/* Status codes of the functions below. */
+enum {
+    GGML_HIP_MOE_OK            = 0,
+    GGML_HIP_MOE_E_INVALID     = -1,  /* bad argument, shape or stride */
+    GGML_HIP_MOE_E_UNSUPPORTED = -2,  /* valid ggml, but a type / shape / fusion this path does not run */
+    GGML_HIP_MOE_E_DEVICE      = -3,  /* a HIP runtime call failed */
+    GGML_HIP_MOE_E_DISABLED    = -4,  /* the cache path was asked for while the cache is off */
+    GGML_HIP_MOE_E_STATE       = -5,  /* wrong state (e.g. src0 not wanted, configure after registration) */
+    GGML_HIP_MOE_E_TIMEOUT     = -6   /* a bounded in-kernel wait gave up (ggml_hip_moe_check_status) */
+};
 
 /* ggml_type values used by the path (ggml.h numbering) */
 enum {
@@ -422,6 +433,19 @@ int ggml_hip_moe_trace_append(const char *path, const char *name, const int32_t 
 
 /* Flushes and closes every trace file opened by ggml_hip_moe_trace_append. */
 int ggml_hip_moe_trace_close(void);
+
+/* Device-side errors of the launches on `stream` since the last call: waits for the
+ * stream, then returns 0, or GGML_HIP_MOE_E_TIMEOUT when a fused gate/up launch
+ * (ggml_hip_moe_ffn_gate_up_norm) had a bounded wait give up -- its workgroups then
+ * skip their rows, so those launches' outputs are not valid -- and clears the
+ * condition.  The word is per GPU (the current device).  No reference counterpart:
+ * the reference's kernel has no in-kernel waits. */
+int ggml_hip_moe_check_status(void *stream);
+
+/* Debug: polls a bounded in-kernel wait makes before it gives up (n < 0: the default,
+ * 2^22).  0 makes every such wait give up at once, which tests the timeout path with
+ * every kernel still exiting normally.  Applies to launches issued after the call. */
+int ggml_hip_moe_debug_set_spin_limit(int64_t n);
 
 /* Text of the last error on this thread. */
 const char *ggml_hip_moe_last_error(void);

@@ -55,14 +55,38 @@ def check_recorder(lib, stream, model: CacheModel, tag: str):
         assert st.tolist() == e.stamps, (tag, e.name)
 
 
+def fusion_from_ptrs(mc_mod, **ptrs):
+    """ggml_hip_moe_fusion from raw addresses (ints); glu_op SWIGLU unless given."""
+    f = mc_mod.Fusion()
+    f.glu_op = ptrs.pop("glu_op", 2)
+    f.shared_type = ptrs.pop("shared_type", -1)
+    for k, v in ptrs.items():
+        setattr(f, k, v)
+    return f
+
+
+GATE_MODES = ("cache", "device", "device_host_desc", "none")
+
+
 def run_scenario(mc_mod, lib, backend, *, n_experts=16, R=40, K=4096, wtype=10, slots=5, steps=12, n_tok=2,
-                 n_used=4, seed_path=None, free_bytes, max_promotions=48, check_outputs=None, rng_seed=1234):
+                 n_used=4, seed_path=None, free_bytes, max_promotions=48, check_outputs=None, rng_seed=1234,
+                 gate_mode="cache", shared_bias=False):
     """backend: object with
          host_tensor(nbytes, role) -> (ptr, keepalive)  GPU-readable host memory holding the weights of `role`
+         device_tensor(nbytes, role) -> (ptr, keepalive) device memory holding the weights of `role`
+         fusion_extra() -> dict of fusion fields (x_bias, shared_up, shared_gate, shared_dst, shared_type,
+                           shared_stride_col_dst) as addresses: a shared expert and a routed bias
          ids_buffer(n_tok, n_used) -> (ptr, setter)     device-visible ids
          act_buffer(n_tok, K), dst_buffer(n_tok, n_used, R) -> ptr
          stream -> c_void_p
-       check_outputs(step, ids) is called after each GEMV when given (GPU backend)."""
+       gate_mode: "cache"  the gate is a host tensor the cache manages (its own entry, stamps and misses);
+                  "device" the gate is device memory passed as fusion->gate;
+                  "device_host_desc" the gate is device memory passed as the host-side gate tensor, which
+                           wants() refuses;
+                  "none"   no gate.
+       Only a cache-managed gate is recorded (kernels/moe-cache.cu:178-201, :804): the model sees gate=None
+       otherwise.  check_outputs(step, ids) is called after each GEMV when given (GPU backend)."""
+    assert gate_mode in GATE_MODES, gate_mode
     rng = np.random.default_rng(rng_seed)
     cfg = mc_mod.Config()
     cfg.enabled, cfg.slots, cfg.budget_gb, cfg.margin_gb = 1, slots, 0.0, 2.0
@@ -75,10 +99,22 @@ def run_scenario(mc_mod, lib, backend, *, n_experts=16, R=40, K=4096, wtype=10, 
     rb = mc_mod.row_bytes(wtype, K)
     eb = rb * R
     up_ptr, up_keep = backend.host_tensor(eb * n_experts, "up")
-    gate_ptr, gate_keep = backend.host_tensor(eb * n_experts, "gate")
     keep = []
     up_t = mc_mod.make_tensor(wtype, K, R, n_experts, up_ptr, name=UP_NAME, keep=keep)
-    gate_t = mc_mod.make_tensor(wtype, K, R, n_experts, gate_ptr, name=GATE_NAME, keep=keep)
+    gate_t, gate_keep, fptrs = None, None, {}
+    if gate_mode == "cache":
+        gate_ptr, gate_keep = backend.host_tensor(eb * n_experts, "gate")
+        gate_t = mc_mod.make_tensor(wtype, K, R, n_experts, gate_ptr, name=GATE_NAME, keep=keep)
+    elif gate_mode == "device_host_desc":
+        gate_ptr, gate_keep = backend.device_tensor(eb * n_experts, "gate")
+        gate_t = mc_mod.make_tensor(wtype, K, R, n_experts, gate_ptr, name=GATE_NAME, keep=keep)
+        assert lib.ggml_hip_moe_cache_wants(C.byref(gate_t)) == 0
+    elif gate_mode == "device":
+        gate_ptr, gate_keep = backend.device_tensor(eb * n_experts, "gate")
+        fptrs["gate"] = gate_ptr
+    if shared_bias:
+        fptrs.update(backend.fusion_extra())
+    fusion = fusion_from_ptrs(mc_mod, **fptrs) if fptrs else None
     assert lib.ggml_hip_moe_cache_wants(C.byref(up_t)) == 1, lib.ggml_hip_moe_last_error()
     assert lib.ggml_hip_moe_cache_active() == 0
 
@@ -89,17 +125,20 @@ def run_scenario(mc_mod, lib, backend, *, n_experts=16, R=40, K=4096, wtype=10, 
     dst_ptr = backend.dst_buffer(n_tok, n_used, R)
     stream = backend.stream
     act_row = K // 32
+    gate_e = None
     for step in range(steps):
         ids = skewed_ids(rng, n_tok, n_used, n_experts)
         set_ids(ids)
         rc = lib.ggml_hip_moe_cache_mul_mat_vec_q(
-            C.byref(up_t), C.byref(gate_t), None, y_ptr, ids_ptr, dst_ptr,
+            C.byref(up_t), C.byref(gate_t) if gate_t is not None else None,
+            C.byref(fusion) if fusion is not None else None, y_ptr, ids_ptr, dst_ptr,
             K, R, n_experts, 1, n_tok, K // mc_mod.BLOCK[wtype][0], eb, eb * n_experts,
             1, n_used, act_row, n_used * R, act_row, R, n_used, stream)
         assert rc == 0, lib.ggml_hip_moe_last_error()
         if step == 0:
             up_e = model.register(up_ptr, UP_NAME, n_experts, eb, free_bytes)
-            gate_e = model.register(gate_ptr, GATE_NAME, n_experts, eb, free_bytes)
+            if gate_mode == "cache":
+                gate_e = model.register(gate_ptr, GATE_NAME, n_experts, eb, free_bytes)
             assert lib.ggml_hip_moe_cache_active() == 1
             compare_state(mc_mod, lib, model, "after registration")
         model.record(up_e, gate_e, ids.tolist())
@@ -113,4 +152,4 @@ def run_scenario(mc_mod, lib, backend, *, n_experts=16, R=40, K=4096, wtype=10, 
         assert lib.ggml_hip_moe_cache_totals(C.byref(tot)) == 0
         assert (tot.last_step_misses, tot.last_step_hits) == model.last, (step, tot.last_step_misses, model.last)
         assert tot.promotions == model.promotions and tot.evictions == model.evictions and tot.clock == model.clock
-    return model, (up_keep, gate_keep, keep, sp)
+    return model, (up_keep, gate_keep, keep, sp, fusion)

@@ -26,14 +26,16 @@ struct SimDevice final : Device {
     std::mutex m;
     std::map<uintptr_t, Region> regions;   // base -> (size, kind)
     size_t free_b = 64ull << 30, total_b = 64ull << 30;
-    long long n_gemv = 0, n_h2d = 0, n_d2h = 0, n_sync = 0, bytes_h2d = 0;
+    long long n_gemv = 0, n_h2d = 0, n_d2h = 0, n_sync = 0, bytes_h2d = 0, n_alloc = 0;
     int fail_alloc_after = -1;            // < 0: never
+    int fail_h2d_after = -1;              // < 0: never
 
     const char *name() const override { return "sim"; }
     int alloc(void **p, size_t n, int kind) {
         std::lock_guard<std::mutex> l(m);
         if (fail_alloc_after == 0) return 2;   // hipErrorOutOfMemory
         if (fail_alloc_after > 0) --fail_alloc_after;
+        n_alloc++;
         void *q = malloc(n ? n : 1);
         if (!q) return 2;
         memset(q, 0xCD, n);
@@ -54,6 +56,8 @@ struct SimDevice final : Device {
     int malloc_host(void **p, size_t n) override { return alloc(p, n, PTR_HOST); }
     int free_host(void *p) override { return release(p); }
     int copy_h2d(void *d, const void *s, size_t n, void *) override {
+        if (fail_h2d_after == 0) return 1;     // hipErrorInvalidValue
+        if (fail_h2d_after > 0) --fail_h2d_after;
         memcpy(d, s, n);
         n_h2d++;
         bytes_h2d += (long long) n;
@@ -107,7 +111,7 @@ struct SimDevice final : Device {
             if (a.stamps) a.stamps[e] = clk;
             const uint32_t mu = (uint32_t) (pu & 1u);
             uint32_t mg = 0, hits = 1u - mu;
-            if (a.tbl_gate) {
+            if (a.tbl_gate && a.cache_id_gate >= 0) {     // a gate without a cache entry is not recorded
                 const uint64_t pg = a.tbl_gate[e];
                 if (a.stamps_gate) a.stamps_gate[e] = clk;
                 mg = (uint32_t) (pg & 1u);
@@ -127,6 +131,11 @@ struct SimDevice final : Device {
     int launch_combine(const CombineArgs &, void *) override { return 98; }
     int launch_mmq(const MmqArgs &, int, void *) override { return 98; }
     int launch_ssm_conv(const SsmConvArgs &, void *) override { return 98; }
+    uint32_t status = 0;                  // no kernel runs here: stays 0 unless a test sets it
+    int status_address(uint32_t **p) override {
+        *p = &status;
+        return 0;
+    }
     const char *error_string(int code) override {
         return code == 2 ? "out of memory (sim)" : code == 98 ? "not simulated" : "sim error";
     }
@@ -163,6 +172,19 @@ void *mc_sim_dev_alloc(uint64_t n) {
 int mc_sim_free(void *p) { return mc::g_sim.release(p); }
 
 void mc_sim_fail_alloc_after(int n) { mc::g_sim.fail_alloc_after = n; }
+
+void mc_sim_fail_h2d_after(int n) { mc::g_sim.fail_h2d_after = n; }
+
+void mc_sim_set_status(uint32_t v) { mc::g_sim.status = v; }
+
+// number of device / pinned allocations made so far (the no-alloc entry must not add any)
+long long mc_sim_alloc_count(void) { return mc::g_sim.n_alloc; }
+
+// live allocations of the simulated device (device, pinned host and registered regions)
+long long mc_sim_live_regions(void) {
+    std::lock_guard<std::mutex> l(mc::g_sim.m);
+    return (long long) mc::g_sim.regions.size();
+}
 
 void mc_sim_counters(long long *out5) {
     out5[0] = mc::g_sim.n_gemv;

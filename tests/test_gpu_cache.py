@@ -15,19 +15,43 @@ pytestmark = pytest.mark.gpu
 
 
 class GpuBackend:
-    def __init__(self, torch, mc, O, n_experts, R, K, wtype, seed):
+    def __init__(self, torch, mc, O, n_experts, R, K, wtype, seed, gate_mode="cache", shared_bias=False):
         self.torch, self.mc, self.O = torch, mc, O
         self.K, self.R, self.wtype, self.n_experts = K, R, wtype, n_experts
+        self.gate_mode, self.shared_bias = gate_mode, shared_bias
         self.w = {"up": H.weights(wtype, n_experts, R, K, seed=seed),
                   "gate": H.weights(wtype, n_experts, R, K, seed=seed + 1)}
         self.stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
         self.keep = []
+        if shared_bias:
+            rng = np.random.default_rng(seed + 2)
+            self.sh_type = 12                                  # Q4_K shared expert
+            self.sh_up = H.weights(self.sh_type, 1, R, K, seed=seed + 3)[0]
+            self.sh_gate = H.weights(self.sh_type, 1, R, K, seed=seed + 4)[0]
+            self.bias = rng.normal(0.0, 0.1, (n_experts, R)).astype(np.float32)
 
     def host_tensor(self, nbytes, role):
         t = self.torch.empty(nbytes, dtype=self.torch.uint8, pin_memory=True)
         t.numpy()[:] = self.w[role].reshape(-1)
         self.keep.append(t)
         return t.data_ptr(), t
+
+    def device_tensor(self, nbytes, role):
+        t = self.torch.from_numpy(self.w[role].reshape(-1)).cuda()
+        self.keep.append(t)
+        return t.data_ptr(), t
+
+    def fusion_extra(self):
+        torch = self.torch
+        self.d_bias = torch.from_numpy(self.bias).cuda()
+        self.d_sh_up = torch.from_numpy(self.sh_up).cuda()
+        self.d_sh_gate = torch.from_numpy(self.sh_gate).cuda()
+        self.sh_dst = torch.zeros((8, self.R), dtype=torch.float32, device="cuda")     # up to 8 tokens
+        f = {"x_bias": self.d_bias.data_ptr(), "shared_up": self.d_sh_up.data_ptr(), "shared_type": self.sh_type,
+             "shared_dst": self.sh_dst.data_ptr(), "shared_stride_col_dst": self.R}
+        if self.gate_mode != "none":
+            f["shared_gate"] = self.d_sh_gate.data_ptr()
+        return f
 
     def ids_buffer(self, n_tok, n_used):
         self.ids = self.torch.zeros((n_tok, n_used), dtype=self.torch.int32, device="cuda")
@@ -46,18 +70,37 @@ class GpuBackend:
         torch, mc, O = self.torch, self.mc, self.O
         torch.cuda.synchronize()
         got = self.dst.cpu().numpy()
+        got_sh = self.sh_dst.cpu().numpy()[:ids.shape[0]] if self.shared_bias else None
         # the same weights resident in device memory, through the no-cache entry point
         ref = torch.zeros_like(self.dst)
         up_d = torch.from_numpy(self.w["up"]).cuda()
-        gate_d = torch.from_numpy(self.w["gate"]).cuda()
-        f = mc.make_fusion(gate=gate_d, glu_op=mc.GLU_SWIGLU)
+        has_gate = self.gate_mode != "none"
+        gate_d = torch.from_numpy(self.w["gate"]).cuda() if has_gate else None
+        kw = {}
+        if self.shared_bias:
+            ref_sh = torch.zeros_like(self.sh_dst)
+            kw = dict(x_bias=self.d_bias, shared_up=self.d_sh_up, shared_gate=self.d_sh_gate if has_gate else None,
+                      shared_dst=ref_sh, shared_type=self.sh_type)
+        f = mc.make_fusion(gate=gate_d, glu_op=mc.GLU_SWIGLU, **kw)
         mc.mul_mat_vec(wtype=self.wtype, weights=up_d, ids=self.ids, y=self.y, dst=ref, K=self.K, R=self.R,
                        n_experts=self.n_experts, fusion=f)
         torch.cuda.synchronize()
         assert np.array_equal(got, ref.cpu().numpy()), f"step {step}: cache path != resident path"
+        if self.shared_bias:
+            assert np.array_equal(got_sh, ref_sh.cpu().numpy()[:ids.shape[0]]), f"step {step}: shared expert differs"
         yb = self.y.cpu().numpy().reshape(ids.shape[0], 1, -1)
+        okw = {}
+        if self.shared_bias:
+            okw = dict(x_bias=self.bias, sh_type=self.sh_type, sh_up=self.sh_up,
+                       sh_gate=self.sh_gate if has_gate else None)
         want = O.mul_mat_id(wtype=self.wtype, K=self.K, R=self.R, n_as=self.n_experts, src0=self.w["up"],
-                            gate=self.w["gate"], ids=ids, act=yb, act_kind=O.ACT_Q8_1, glu_op=O.GLU_SWIGLU)
+                            gate=self.w["gate"] if has_gate else None, ids=ids, act=yb, act_kind=O.ACT_Q8_1,
+                            glu_op=O.GLU_SWIGLU, **okw)
+        if self.shared_bias:
+            want, want_sh = want
+            # the shared expert takes no routed bias (the reference's shared row indexes expert 0's bias,
+            # kernels/moe-cache.cu:244 with :143)
+            assert O.rel_l2(got_sh, want_sh) <= H.TOL_SAME
         assert O.rel_l2(got, want) <= H.TOL_SAME
 
 
@@ -78,6 +121,27 @@ def test_cache_scenario_gpu(torch_gpu, mc, O, tmp_path, wtype, slots, seeded):
     assert model.promotions > 0
     if slots < n_experts:
         assert model.evictions > 0
+    torch.cuda.synchronize()
+    assert mc.lib().ggml_hip_moe_cache_reset() == 0
+
+
+@pytest.mark.parametrize("gate_mode,shared_bias", [("device", False), ("device_host_desc", False), ("none", False),
+                                                    ("cache", True), ("device", True)])
+def test_cache_gate_modes_gpu(torch_gpu, mc, O, gate_mode, shared_bias):
+    """Host-resident up with a gate the cache does not manage (device memory as fusion->gate, or a
+    device tensor given as the host-side gate, which wants() refuses): the gate leaves no stamps, hits or
+    misses (kernels/moe-cache.cu:178-201, :804) and is addressed per expert (the reference reads expert 0's
+    gate there, :199-201).  With a shared expert and a routed bias, the shared expert takes no bias.
+    Recorder and LRU state vs the cache model; outputs vs the resident path and the oracle."""
+    torch = torch_gpu
+    print(f"cache gate mode {gate_mode} shared_bias={shared_bias}", flush=True)
+    n_experts, R, K, wtype = 16, 64, 2048, 10
+    be = GpuBackend(torch, mc, O, n_experts, R, K, wtype, seed=950, gate_mode=gate_mode, shared_bias=shared_bias)
+    free_b = torch.cuda.mem_get_info()[0]
+    model, keep = S.run_scenario(mc, mc.lib(), be, n_experts=n_experts, R=R, K=K, wtype=wtype, slots=5, steps=8,
+                                 n_tok=2, n_used=4, free_bytes=free_b, check_outputs=be.check_outputs, rng_seed=17,
+                                 gate_mode=gate_mode, shared_bias=shared_bias)
+    assert model.promotions > 0
     torch.cuda.synchronize()
     assert mc.lib().ggml_hip_moe_cache_reset() == 0
 

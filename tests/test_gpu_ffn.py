@@ -339,3 +339,43 @@ def test_fused_block_through_the_cache(torch_gpu, mc):
     tot = mc.totals()
     assert tot.promotions > 0 and tot.hits > 0
     mc.reset()
+
+
+def test_gate_up_norm_timeout_reports_status(torch_gpu, mc):
+    """A bounded wait that gives up is reported, not silent: with the debug spin limit 0 every wait of the
+    fused gate/up kernel gives up at once (every kernel still exits: the waits poll zero times), and
+    ggml_hip_moe_check_status returns E_TIMEOUT once, then 0.  With the default limit the same launch
+    matches the op-by-op path and reports nothing."""
+    torch = torch_gpu
+    md = import_module("a6000_custom_kernels_amd.moe_decode")
+    _note("gate_up_norm timeout status")
+    E, U, K, R, n_tok, eps = 8, 4, 1024, 64, 1, 1e-6
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(91)
+    up = md.random_expert_tensor(torch, mc.Q2_K, E, R, K, gen)
+    gate = md.random_expert_tensor(torch, mc.Q2_K, E, R, K, gen)
+    rng = np.random.default_rng(92)
+    x = torch.from_numpy(rng.standard_normal((n_tok, K)).astype(np.float32)).cuda()
+    ids = torch.from_numpy(np.array([[0, 3, 5, 7]], np.int32)).cuda()
+    f = mc.make_fusion(gate=gate, glu_op=mc.GLU_SWIGLU)
+    assert mc.check_status() == 0                      # nothing pending from earlier tests
+    dst = torch.full((n_tok, U, R), SENTINEL, dtype=torch.float32, device="cuda")
+    try:
+        assert mc.lib().ggml_hip_moe_debug_set_spin_limit(0) == 0
+        mc.ffn_gate_up_norm(wtype=mc.Q2_K, weights=up, ids=ids, x=x, dst=dst, K=K, R=R, n_experts=E, eps=eps,
+                            fusion=f)
+    finally:
+        mc.lib().ggml_hip_moe_debug_set_spin_limit(-1)
+    rc = mc.check_status()
+    assert rc == mc.E_TIMEOUT, rc
+    assert b"gave up" in mc.lib().ggml_hip_moe_last_error()
+    assert bool((dst == SENTINEL).all())               # every step skipped its rows
+    assert mc.check_status() == 0                      # cleared
+    mc.ffn_gate_up_norm(wtype=mc.Q2_K, weights=up, ids=ids, x=x, dst=dst, K=K, R=R, n_experts=E, eps=eps, fusion=f)
+    assert mc.check_status() == 0
+    y_ref = _norm_q8_1(torch, mc, x, None, eps)
+    dst_ref = torch.zeros_like(dst)
+    mc.mul_mat_vec(wtype=mc.Q2_K, weights=up, ids=ids, y=y_ref.view(n_tok, 1, -1), dst=dst_ref, K=K, R=R,
+                   n_experts=E, fusion=f)
+    torch.cuda.synchronize()
+    assert torch.equal(dst, dst_ref)

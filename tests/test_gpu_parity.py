@@ -107,10 +107,15 @@ def test_gemv_cpu_mode_matches_ggml_cpu(torch_gpu, mc, O, wtype):
     err = O.rel_l2(got, want)
     _note(f"  rel_l2 vs ggml-cpu={err:.3e}")
     assert err <= H.TOL_CPU
-    # and the default q8_1 boundary format, reported beside it
+    # and the default q8_1 boundary format, beside it.  Legacy types: q8_1 codes equal ggml-CPU's q8_0
+    # codes, so only the fp32 summation order differs.  K-quants: 32-value q8_1 scales against ggml-CPU's
+    # one q8_K scale per 256 values, two independent 8-bit roundings of x; the oracle measures 7.9e-3 to
+    # 8.2e-3 on these inputs for Q2_K..Q6_K.
     yq1 = mc.quantize_q8_1(xd).cpu().numpy().reshape(n_tok, 1, -1)
     got1 = _run_gemv(torch, mc, wtype, w, ids, yq1, K, R, n_exp, mc.ACT_Q8_1)
-    _note(f"  q8_1-mode rel_l2 vs ggml-cpu={O.rel_l2(got1, want):.3e}")
+    err1 = O.rel_l2(got1, want)
+    _note(f"  q8_1-mode rel_l2 vs ggml-cpu={err1:.3e}")
+    assert err1 <= (H.TOL_Q8_1_VS_CPU if wtype in mc.KQUANTS else H.TOL_SAME)
 
 
 @pytest.mark.parametrize("glu_op", [2, 0, 1, 3, 4, 5, 6])

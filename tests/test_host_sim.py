@@ -31,6 +31,8 @@ def sim(mc):
     lib.mc_sim_dev_alloc.restype, lib.mc_sim_dev_alloc.argtypes = C.c_void_p, [C.c_uint64]
     lib.mc_sim_set_mem_info.argtypes = [C.c_uint64, C.c_uint64]
     lib.mc_sim_fail_alloc_after.argtypes = [C.c_int]
+    lib.mc_sim_fail_h2d_after.argtypes = [C.c_int]
+    lib.mc_sim_live_regions.restype = C.c_longlong
     lib.mc_sim_counters.argtypes = [C.c_void_p]
     return lib
 
@@ -44,6 +46,19 @@ class SimBackend:
         p = self.lib.mc_sim_host_alloc(nbytes)
         assert p
         return p, p
+
+    def device_tensor(self, nbytes, role):
+        p = self.lib.mc_sim_dev_alloc(nbytes)
+        assert p
+        return p, p
+
+    def fusion_extra(self):
+        R = 64
+        bias = self.lib.mc_sim_dev_alloc(4 * R * 64)
+        sh = self.lib.mc_sim_dev_alloc(1 << 16)
+        sh_dst = self.lib.mc_sim_dev_alloc(4 * R * 8)
+        return {"x_bias": bias, "shared_up": sh, "shared_gate": sh, "shared_dst": sh_dst, "shared_type": 12,
+                "shared_stride_col_dst": R}
 
     def ids_buffer(self, n_tok, n_used):
         self.ids = np.zeros((n_tok, n_used), np.int32)
@@ -73,6 +88,66 @@ def test_sim_scenario_matches_model(sim, mc, tmp_path, slots, steps, n_tok, n_us
                                  max_promotions=max_promo, rng_seed=rseed)
     if slots:
         assert model.promotions > 0
+
+
+@pytest.mark.parametrize("gate_mode,shared_bias", [("device", False), ("device_host_desc", False), ("none", False),
+                                                    ("cache", True), ("device", True)])
+def test_sim_gate_modes_match_model(sim, mc, gate_mode, shared_bias):
+    """A gate the cache does not manage (device memory as fusion->gate, or a device tensor that wants()
+    refuses) and no gate at all leave no gate stamps, hits or misses (kernels/moe-cache.cu:178-201, :804):
+    the model records the up tensor only.  A shared expert with a routed bias changes nothing recorded."""
+    sim.mc_sim_set_mem_info(64 << 30, 64 << 30)
+    model, keep = S.run_scenario(mc, sim, SimBackend(sim), n_experts=16, R=8, K=256, wtype=10, slots=5, steps=20,
+                                 n_tok=2, n_used=4, free_bytes=64 << 30, rng_seed=11, gate_mode=gate_mode,
+                                 shared_bias=shared_bias)
+    assert len(model.entries) == (2 if gate_mode == "cache" else 1)
+    assert model.promotions > 0 and model.evictions > 0
+
+
+@pytest.mark.parametrize("fail_after,what", [(4, b"table upload"), (2, b"seed copy")])
+def test_sim_failed_registration_leaves_nothing(sim, mc, tmp_path, fail_after, what):
+    """A failing seed copy or table upload frees the pool, table and stamps and registers nothing, so a
+    later call registers the tensor afresh (never an entry whose device table was not written)."""
+    be = SimBackend(sim)
+    assert sim.ggml_hip_moe_cache_reset() == 0
+    seed_path = str(tmp_path / "seed.txt")
+    with open(seed_path, "w") as f:
+        f.write("x 3,1,2,0\n")
+    cfg = mc.Config()
+    sp = seed_path.encode()
+    cfg.enabled, cfg.slots, cfg.budget_gb, cfg.margin_gb, cfg.seed_path, cfg.max_promotions = 1, 4, 0.0, 0.0, sp, 48
+    assert sim.ggml_hip_moe_cache_configure(C.byref(cfg)) == 0
+    sim.mc_sim_set_mem_info(64 << 30, 64 << 30)
+    K, R, n = 256, 8, 8
+    eb = mc.row_bytes(mc.Q2_K, K) * R
+    keep = []
+    p = be.host_tensor(eb * n, "up")[0]
+    t = mc.make_tensor(mc.Q2_K, K, R, n, p, name="x", keep=keep)
+    ids_p, set_ids = be.ids_buffer(1, 2)
+    set_ids(np.array([[0, 1]], np.int32))
+    y, d = be.act_buffer(1, K), be.dst_buffer(1, 2, R)
+    args = (K, R, n, 1, 1, 1, eb, eb * n, 1, 2, 8, 2 * R, 8, R, 2, be.stream)
+    # the first call creates the global stats/clock (3 regions); measure the live regions after that
+    assert sim.ggml_hip_moe_cache_mul_mat_vec_q(C.byref(t), None, None, y, ids_p, d, *args) == 0
+    assert sim.ggml_hip_moe_cache_reset() == 0
+    assert sim.ggml_hip_moe_cache_configure(C.byref(cfg)) == 0
+    base = sim.mc_sim_live_regions()
+    # the registration's H2D copies are seed 3, seed 1, seed 2, seed 0, then the table: fail_after of
+    # them succeed and the next one fails
+    sim.mc_sim_fail_h2d_after(fail_after)
+    rc = sim.ggml_hip_moe_cache_mul_mat_vec_q(C.byref(t), None, None, y, ids_p, d, *args)
+    sim.mc_sim_fail_h2d_after(-1)
+    assert rc < 0 and what in sim.ggml_hip_moe_last_error()
+    assert sim.ggml_hip_moe_cache_num_entries() == 0
+    # stats/clock/pinned stats of this configuration remain; nothing of the failed entry does
+    assert sim.mc_sim_live_regions() == base + 3
+    assert sim.ggml_hip_moe_cache_mul_mat_vec_q(C.byref(t), None, None, y, ids_p, d, *args) == 0
+    assert sim.ggml_hip_moe_cache_num_entries() == 1
+    expert_of = np.empty(4, np.int32)
+    assert sim.ggml_hip_moe_cache_entry_slots(0, None, 0, expert_of.ctypes.data, 4) == 0
+    assert expert_of.tolist() == [3, 1, 2, 0]
+    assert sim.ggml_hip_moe_cache_reset() == 0
+    assert sim.mc_sim_live_regions() == base
 
 
 def test_sim_budget_and_free_memory_clamp(sim, mc):
