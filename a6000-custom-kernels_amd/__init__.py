@@ -117,6 +117,8 @@ SIGNATURES = [
     ("ggml_hip_moe_mul_mat_id", C.c_int,
      [C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor),
       C.POINTER(Fusion), _VP, _I64, _VP]),
+    ("ggml_hip_moe_mul_mat_id_noalloc", C.c_int,
+     [C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Fusion), _VP]),
     ("ggml_hip_ssm_conv_f32", C.c_int,
      [_VP, _I64, _I64, _I64, _VP, C.c_int32, _I64, _VP, C.c_int32, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
       _VP]),

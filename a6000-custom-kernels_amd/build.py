@@ -39,6 +39,7 @@ SOURCES = [
     ("mc_mmq.hip", "hip"),
     ("mc_ffn.hip", "hip"),
     ("mc_ssm_conv.hip", "hip"),
+    ("mc_noalloc.hip", "hip"),
     ("mc_device_hip.cpp", "hiphost"),
     ("mc_host.cpp", "cxx"),
 ]

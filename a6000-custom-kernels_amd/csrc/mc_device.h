@@ -37,6 +37,7 @@ struct Device {
     virtual int launch_mmq(const MmqArgs &m, int type, void *stream) = 0;
     virtual int launch_ssm_conv(const SsmConvArgs &a, void *stream) = 0;
     virtual int status_address(uint32_t **p) = 0;                          // device status word of the current device
+    virtual int scratch_address(void **p, size_t *bytes) = 0;              // no-alloc scratch of the current device
     virtual const char *error_string(int code) = 0;
 };
 

@@ -11,6 +11,7 @@ int launch_combine(const CombineArgs &c, void *stream);               // mc_kern
 int launch_mmq(const MmqArgs &m, int type, void *stream);            // mc_mmq.hip
 int launch_ssm_conv(const SsmConvArgs &a, void *stream);              // mc_ssm_conv.hip
 int status_address(uint32_t **p);                                     // mc_ffn.hip
+int scratch_address(void **p, size_t *bytes);                         // mc_noalloc.hip
 
 namespace {
 
@@ -60,6 +61,7 @@ struct HipDevice final : Device {
     int launch_mmq(const MmqArgs &m, int type, void *s) override { return mc::launch_mmq(m, type, s); }
     int launch_ssm_conv(const SsmConvArgs &a, void *s) override { return mc::launch_ssm_conv(a, s); }
     int status_address(uint32_t **p) override { return mc::status_address(p); }
+    int scratch_address(void **p, size_t *bytes) override { return mc::scratch_address(p, bytes); }
     const char *error_string(int code) override { return hipGetErrorString((hipError_t) code); }
 };
 

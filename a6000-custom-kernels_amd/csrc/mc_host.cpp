@@ -1100,6 +1100,28 @@ int ggml_hip_moe_mul_mat_id(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_
     return mmid_run(p, src0, src1, ids, dst, gate_host, fusion, (uint8_t *) workspace, stream, false);
 }
 
+int ggml_hip_moe_mul_mat_id_noalloc(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *src1,
+                                    const ggml_hip_moe_tensor *ids, const ggml_hip_moe_tensor *dst,
+                                    const ggml_hip_moe_fusion *fusion, void *stream) {
+    if (!dst) return fail(E_INVALID, "mul_mat_id_noalloc: null dst");
+    MmidPlan p;
+    int rc;
+    if ((rc = mmid_plan(src0, src1, ids, dst, nullptr, fusion, p))) return rc;
+    if (p.cache)
+        return fail(E_UNSUPPORTED, "mul_mat_id_noalloc: host-resident experts take the cache path, whose registration "
+                    "allocates the HBM pool; this entry takes device-resident experts only");
+    void *ws = nullptr;
+    size_t cap = 0;
+    if ((rc = dev()->scratch_address(&ws, &cap))) return dev_err(rc, "scratch lookup");
+    const uint64_t need = p.y_bytes + p.ws_mmq;
+    if (need > (uint64_t) cap)
+        return fail(E_UNSUPPORTED, "mul_mat_id_noalloc: this call needs %llu bytes of workspace, the library's "
+                    "scratch holds %llu (use ggml_hip_moe_mul_mat_id with a workspace of that size)",
+                    (unsigned long long) need, (unsigned long long) cap);
+    if (p.n_tok == 0) return 0;
+    return mmid_run(p, src0, src1, ids, dst, nullptr, fusion, (uint8_t *) ws, stream, true);
+}
+
 int ggml_hip_ssm_conv_f32(const float *src0, int64_t src0_nb0, int64_t src0_nb1, int64_t src0_nb2, const void *src1,
                           int32_t src1_type, int64_t src1_nb1, const float *bias, int32_t fuse_silu, float *dst,
                           int64_t dst_nb0, int64_t dst_nb1, int64_t dst_nb2, int64_t nc, int64_t nr, int64_t n_t,

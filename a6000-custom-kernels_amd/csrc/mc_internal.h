@@ -159,6 +159,11 @@ struct GemvArgs {
     int32_t spin_limit;           // iterations of a bounded in-kernel wait before it gives up
 };
 
+// Bytes of the per-GPU device scratch of ggml_hip_moe_mul_mat_id_noalloc (mc_noalloc.hip):
+// enough for the 512-token prefill of a 512-expert layer with 4096-value rows
+// (q8_K rows 2.4 MB + grouped-GEMM workspace 54.6 MB).
+constexpr uint64_t NOALLOC_SCRATCH_BYTES = 64ull << 20;
+
 // Device status bits (ggml_hip_moe_check_status).
 constexpr uint32_t STATUS_WAIT_TIMEOUT = 1u;   // a bounded wait of the fused gate/up kernel gave up
 constexpr int32_t DEFAULT_SPIN_LIMIT = 1 << 22;

@@ -394,6 +394,21 @@ int ggml_hip_moe_mul_mat_id(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_
                             const ggml_hip_moe_tensor *gate_host, const ggml_hip_moe_fusion *fusion,
                             void *workspace, int64_t workspace_bytes, void *stream);
 
+/* ggml_hip_moe_mul_mat_id for callers that cannot allocate (code under graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): no
+ * counterpart in the reference.  Same arguments and results as
+ * ggml_hip_moe_mul_mat_id without gate_host and workspace: the workspace is a
+ * library-held device array of 64 MiB per GPU (kept until the process ends), and
+ * no call allocates.  Device-resident experts only (host-resident experts take
+ * the cache path, whose registration allocates: GGML_HIP_MOE_E_UNSUPPORTED); a
+ * call whose ggml_hip_moe_mul_mat_id_workspace_bytes exceeds 64 MiB returns
+ * GGML_HIP_MOE_E_UNSUPPORTED.  Every call on one GPU uses the same array: calls
+ * that overlap on one GPU (concurrent streams, or another thread) race; calls
+ * ordered on one stream do not. */
+int ggml_hip_moe_mul_mat_id_noalloc(const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *src1,
+                                    const ggml_hip_moe_tensor *ids, const ggml_hip_moe_tensor *dst,
+                                    const ggml_hip_moe_fusion *fusion, void *stream);
+
 /* ---------------------------------------------------------------------
  * SSM_CONV with F32 or F16 conv weights (kernels/ssm-conv.cu:117-217: the
  * reference's ssm_conv_f32_cuda / ggml_cuda_op_ssm_conv, templated on the

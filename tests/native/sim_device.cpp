@@ -131,6 +131,14 @@ struct SimDevice final : Device {
     int launch_combine(const CombineArgs &, void *) override { return 98; }
     int launch_mmq(const MmqArgs &, int, void *) override { return 98; }
     int launch_ssm_conv(const SsmConvArgs &, void *) override { return 98; }
+    // stand-in for the no-alloc scratch: a fixed host block (kernels never run here)
+    size_t scratch_bytes = 1u << 20;
+    alignas(256) static inline unsigned char scratch_block[1u << 20];
+    int scratch_address(void **p, size_t *bytes) override {
+        *p = scratch_block;
+        *bytes = scratch_bytes;
+        return 0;
+    }
     uint32_t status = 0;                  // no kernel runs here: stays 0 unless a test sets it
     int status_address(uint32_t **p) override {
         *p = &status;
