@@ -23,6 +23,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import importlib.util
 import json
 import os
@@ -33,6 +34,7 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 PKG_DIR = ROOT / "a6000-custom-kernels_amd"
 PEAK_HBM_GBS = 8000.0
+PEAK_INT8_OPS = 5.0e15        # MI355X dense int8 MFMA
 METRIC = "MoE GEMV achieved HBM GB/s (% of peak) + 48-layer MoE decode tok/s"
 
 
@@ -178,6 +180,250 @@ def _cpu_layer_loop(O, model, mats, ids, w, nth, budget_s):
     return n, el
 
 
+def graph_ms(torch, launches, rounds):
+    """Mean ms of one pass over `launches` (callables issuing kernels), captured as one graph and replayed
+    `rounds` times between two events on the replay stream (host launch cost excluded)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for f in launches:                    # first use builds every device table
+            f()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for f in launches:
+                f()
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(rounds):
+            g.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / rounds
+
+
+def _rate(nbytes, ms):
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"us": round(ms * 1000, 3), "bytes": int(nbytes), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+
+
+def wl_decode_q4_0(torch, mc, md, rounds, cpu_s=3.0):
+    """One decode MUL_MAT_ID: 64 experts Q4_0 [1024 x 2048], batch 1, top-8, q8_1 activations, all resident.
+    16 copies of the 75 MB expert tensor rotate (1.2 GB) so the 256 MB MALL cannot serve repeat reads."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as O
+    E, K, R, U, copies = 64, 2048, 1024, 8, 16
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(11)
+    ws = [md.random_expert_tensor(torch, mc.Q4_0, E, R, K, gen) for _ in range(copies)]
+    eb = mc.row_bytes(mc.Q4_0, K) * R
+    x = torch.randn((1, K), generator=gen, device="cuda")
+    y = mc.quantize_q8_1(x)
+    ids_np, _ = md.make_routing(copies, 1, E, U, seed=12)
+    ids = [torch.from_numpy(ids_np[i]).cuda() for i in range(copies)]
+    dst = torch.zeros((1, U, R), dtype=torch.float32, device="cuda")
+    launches = [lambda i=i: mc.mul_mat_vec(wtype=mc.Q4_0, weights=ws[i], ids=ids[i], y=y, dst=dst, K=K, R=R,
+                                           n_experts=E) for i in range(copies)]
+    ms = graph_ms(torch, launches, rounds) / copies
+    nbytes = U * eb + y.numel() + U * R * 4
+    out = {"workload": "decode MUL_MAT_ID GEMV, 64 experts Q4_0 [1024 x 2048], B=1, top-8, q8_1, resident",
+           "kernel": "mc_gemv_kernel<q4_0, none, q8_1>", **_rate(nbytes, ms)}
+    if cpu_s > 0:
+        nth = int(os.environ.get("OMP_NUM_THREADS", "0")) or O.cpu_cores()
+        w0, xs = ws[0].cpu().numpy(), x.cpu().numpy()
+        t0, n = time.perf_counter(), 0
+        while time.perf_counter() - t0 < cpu_s:
+            O.cpu_mul_mat_id_f32(wtype=mc.Q4_0, K=K, R=R, n_as=E, src0=w0, src1=xs, ids=ids_np[n % copies],
+                                 nthreads=nth)
+            n += 1
+        el = (time.perf_counter() - t0) / n
+        out["cpu_baseline"] = {"us_per_call": round(el * 1e6, 1), "GB/s": round(nbytes / el / 1e9, 2), "cores": nth,
+                               "kind": "port", "sample": f"{n} calls of the oracle's ggml-CPU MUL_MAT_ID on copy 0"}
+    del ws
+    torch.cuda.empty_cache()
+    return out
+
+
+def wl_type_batch(torch, mc, md, rounds, batches=(1, 8)):
+    """The 512-expert layer (hidden 4096, ffn 768, top-8) for Q4_0, Q5_0, Q8_0, Q3_K, Q4_K, Q5_K, Q6_K experts at
+    `batches` tokens: gate/up GEMV (SwiGLU, per-expert bias and scale on both projections) + down GEMV (bias and
+    scale) from the fp32 GLU rows, 16 seeded routings per point.  Bytes = unique experts x (gate + up + down) +
+    activations + outputs."""
+    import numpy as np
+    E, H, F, U, sets = 512, 4096, 768, 8, 16
+    types = [("q4_0", mc.Q4_0), ("q5_0", mc.Q5_0), ("q8_0", mc.Q8_0), ("q3_K", mc.Q3_K), ("q4_K", mc.Q4_K),
+             ("q5_K", mc.Q5_K), ("q6_K", mc.Q6_K)]
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(21)
+    rng = np.random.default_rng(22)
+    dev = lambda a: torch.from_numpy(a.astype(np.float32)).cuda()
+    xb, gb = dev(rng.standard_normal((E, F)) * 0.1), dev(rng.standard_normal((E, F)) * 0.1)
+    xs, gs = dev(rng.uniform(0.5, 1.5, E)), dev(rng.uniform(0.5, 1.5, E))
+    db, ds = dev(rng.standard_normal((E, H)) * 0.1), dev(rng.uniform(0.5, 1.5, E))
+    rows = []
+    for name, t in types:
+        gate = md.random_expert_tensor(torch, t, E, F, H, gen)
+        up = md.random_expert_tensor(torch, t, E, F, H, gen)
+        down = md.random_expert_tensor(torch, t, E, H, F, gen)
+        eb_gu, eb_dn = mc.row_bytes(t, H) * F, mc.row_bytes(t, F) * H
+        for B in batches:
+            ids_np, _ = md.make_routing(sets * B, 1, E, U, seed=100 + B)
+            ids_np = ids_np.reshape(sets, B, U)
+            x = torch.randn((B, H), generator=gen, device="cuda")
+            y = mc.quantize_q8_1(x)
+            h = torch.zeros((B, U, F), dtype=torch.float32, device="cuda")
+            o = torch.zeros((B, U, H), dtype=torch.float32, device="cuda")
+            f_gu = mc.make_fusion(gate=gate, glu_op=mc.GLU_SWIGLU, x_bias=xb, gate_bias=gb, x_scale=xs, gate_scale=gs)
+            f_dn = mc.make_fusion(x_bias=db, x_scale=ds)
+            ids = [torch.from_numpy(np.ascontiguousarray(ids_np[i])).cuda() for i in range(sets)]
+
+            def step(i):
+                mc.mul_mat_vec(wtype=t, weights=up, ids=ids[i], y=y, dst=h, K=H, R=F, n_experts=E, fusion=f_gu)
+                mc.mul_mat_vec(wtype=t, weights=down, ids=ids[i], y=h, dst=o, K=F, R=H, n_experts=E, fusion=f_dn,
+                               act=mc.ACT_F32, nchannels_y=U)
+
+            ms = graph_ms(torch, [lambda i=i: step(i) for i in range(sets)], rounds) / sets
+            uniq = float(np.mean([len(np.unique(ids_np[i])) for i in range(sets)]))
+            nbytes = uniq * (2 * eb_gu + eb_dn) + y.numel() + h.numel() * 8 + o.numel() * 4
+            rows.append({"type": name, "batch": B, "unique_experts": round(uniq, 2), **_rate(nbytes, ms)})
+            log(f"  type x batch: {name} B={B}: {rows[-1]['us']} us per layer, {rows[-1]['GB/s']} GB/s")
+        del gate, up, down
+        torch.cuda.empty_cache()
+    return {"workload": "512-expert layer (hidden 4096, ffn 768, top-8), gate/up + SwiGLU + bias/scale GEMV and "
+                        "down + bias/scale GEMV, per type and batch; us/bytes per layer",
+            "points": rows}
+
+
+def wl_prefill(torch, mc, md, rounds, wtype=None):
+    """512 tokens x top-8 over 512 Q4_K experts (hidden 4096, ffn 768): q8_K of x, grouped int8-MFMA gate/up GEMM
+    with SwiGLU, q8_K of the GLU rows, grouped down GEMM."""
+    wtype = wtype if wtype is not None else mc.Q4_K
+    E, H, F, U, T = 512, 4096, 768, 8, 512
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(31)
+    gate = md.random_expert_tensor(torch, wtype, E, F, H, gen)
+    up = md.random_expert_tensor(torch, wtype, E, F, H, gen)
+    down = md.random_expert_tensor(torch, wtype, E, H, F, gen)
+    ids_np, _ = md.make_routing(T, 1, E, U, seed=32)
+    ids = torch.from_numpy(ids_np.reshape(T, U)).cuda()
+    x = torch.randn((T, H), generator=gen, device="cuda")
+    yx = torch.zeros(T * H // 256 * 292 + 256, dtype=torch.uint8, device="cuda")
+    h = torch.zeros((T, U, F), dtype=torch.float32, device="cuda")
+    yh = torch.zeros(T * U * F // 256 * 292 + 256, dtype=torch.uint8, device="cuda")
+    o = torch.zeros((T, U, H), dtype=torch.float32, device="cuda")
+    nws = max(int(mc.lib().ggml_hip_moe_mul_mat_q_workspace_bytes(H, E, T * U)),
+              int(mc.lib().ggml_hip_moe_mul_mat_q_workspace_bytes(F, E, T * U)))
+    ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
+    s = lambda: C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def q_x():
+        mc.check(mc.lib().ggml_hip_quantize_q8_K(x.data_ptr(), yx.data_ptr(), H, T, H, H // 256, s()), "q8_K x")
+
+    def gu():
+        mc.mul_mat_q(wtype=wtype, weights=up, gate=gate, ids=ids, y=yx, dst=h, K=H, R=F, n_experts=E, workspace=ws)
+
+    def q_h():
+        mc.check(mc.lib().ggml_hip_quantize_q8_K(h.data_ptr(), yh.data_ptr(), F, T * U, F, F // 256, s()), "q8_K h")
+
+    def dn():
+        mc.mul_mat_q(wtype=wtype, weights=down, ids=ids, y=yh, dst=o, K=F, R=H, n_experts=E, nchannels_y=U,
+                     workspace=ws)
+
+    ms_all = graph_ms(torch, [q_x, gu, q_h, dn], rounds)
+    ms_gu = graph_ms(torch, [gu], rounds)
+    ms_dn = graph_ms(torch, [dn], rounds)
+    eb = mc.row_bytes(wtype, H) * F
+    touched = len(set(ids_np.reshape(-1).tolist()))
+    wbytes = touched * 3 * eb
+    ops = 2 * T * U * 3 * F * H
+    out = {"workload": f"prefill FFN, {T} tokens x top-{U} of {E} experts ({mc.TYPE_NAMES[wtype]}, hidden {H}, "
+                       f"ffn {F}): q8_K activations, grouped int8-MFMA GEMMs; us/bytes per layer",
+           **_rate(wbytes, ms_all), "us_gate_up": round(ms_gu * 1000, 1), "us_down": round(ms_dn * 1000, 1),
+           "experts_touched": touched, "int8_ops": ops, "TOP/s": round(ops / (ms_all * 1e-3) / 1e12, 2),
+           "mfma_frac": round(ops / (ms_all * 1e-3) / PEAK_INT8_OPS, 4), "tok_per_s": round(T / (ms_all * 1e-3), 1)}
+    del gate, up, down, ws
+    torch.cuda.empty_cache()
+    return out
+
+
+def wl_table_gate_up(torch, mc, md, rounds, layers=8, routings=4):
+    """The pointer-table GEMV itself (ggml_hip_moe_cache_mul_mat_vec_q): gate/up + SwiGLU over 512 Q2_K experts
+    (hidden 4096, ffn 768), top-8, B=1, every table entry LSB=0 (the pool holds every expert, seeded), the pick
+    recorder on.  `layers` layers of gate/up tensors in pinned host memory, `routings` routings per layer, one
+    graph of layers x routings launches (~530 MB of distinct expert reads per replay, past the MALL)."""
+    import numpy as np
+    import tempfile
+    E, H, F, U = 512, 4096, 768, 8
+    t = mc.Q2_K
+    eb = mc.row_bytes(t, H) * F
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(51)
+    keep, tens = [], {}
+    seed_path = os.path.join(tempfile.mkdtemp(), "moe_seed_all.txt")
+    all_ids = ",".join(str(e) for e in range(E))
+    with open(seed_path, "w") as f:
+        for l in range(layers):
+            for role in ("gate", "up"):
+                f.write(f"blk.{l}.ffn_{role}_exps.weight {all_ids}\n")
+    for l in range(layers):
+        for role in ("gate", "up"):
+            dev = md.random_expert_tensor(torch, t, E, F, H, gen)
+            p = torch.empty(E * eb, dtype=torch.uint8, pin_memory=True)
+            p.copy_(dev.view(-1))
+            del dev
+            keep.append(p)
+            tens[(l, role)] = mc.make_tensor(t, H, F, E, p.data_ptr(), name=f"blk.{l}.ffn_{role}_exps.weight", keep=keep)
+    mc.reset()
+    mc.configure(enabled=True, slots=-1, budget_gb=0.0, margin_gb=2.0, seed_path=seed_path, max_promotions=48)
+    ids_np, _ = md.make_routing(routings, layers, E, U, seed=52)
+    ids = torch.from_numpy(ids_np).cuda()                      # [routings, layers, U]
+    x = torch.randn((1, H), generator=gen, device="cuda")
+    y = mc.quantize_q8_1(x)
+    h = torch.zeros((1, U, F), dtype=torch.float32, device="cuda")
+    lib, ar = mc.lib(), H // 32
+
+    def launch(r, l):
+        sp = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        mc.check(lib.ggml_hip_moe_cache_mul_mat_vec_q(
+            C.byref(tens[(l, "up")]), C.byref(tens[(l, "gate")]), None, y.data_ptr(), ids[r, l].data_ptr(),
+            h.data_ptr(), H, F, E, 1, 1, H // 256, eb, eb * E, 1, U, ar, U * F, ar, F, U, sp), "table gate/up")
+
+    ms = graph_ms(torch, [lambda r=r, l=l: launch(r, l) for r in range(routings) for l in range(layers)],
+                  rounds) / (routings * layers)
+    stats = mc.stats_snapshot(2)
+    assert int(stats[0]) == 0, f"all-hit run recorded {int(stats[0])} misses"
+    nbytes = 2 * U * eb + y.numel() + U * F * 4
+    out = {"workload": "pointer-table GEMV (cache path), gate/up + SwiGLU, 512 Q2_K experts [768 x 4096], top-8, "
+                       "B=1, every table entry in the HBM pool (LSB=0), pick recorder on",
+           "kernel": "mc_gemv_kernel<q2_K, none, q8_1> with tbl/tbl_gate, stamps and stats",
+           **_rate(nbytes, ms), "misses": int(stats[0]), "hits_recorded": int(stats[1])}
+    mc.reset()
+    del keep
+    torch.cuda.empty_cache()
+    return out
+
+
+WORKLOADS = {"decode_q4_0": wl_decode_q4_0, "type_batch": wl_type_batch, "prefill": wl_prefill,
+             "table_gate_up": wl_table_gate_up}
+
+
+def run_workloads(torch, mc, md, names, args):
+    """The secondary workloads, each as one entry: us / bytes / GB/s / frac of its dominant unit."""
+    res = {}
+    for name in names:
+        t0 = time.perf_counter()
+        fn = WORKLOADS[name]
+        res[name] = fn(torch, mc, md, args.kernel_rounds) if name != "decode_q4_0" else \
+            fn(torch, mc, md, args.kernel_rounds, cpu_s=0.0 if args.no_cpu else 3.0)
+        r = res[name]
+        log(f"workload {name}: " + (f"{r['us']} us, {r['GB/s']} GB/s" if "us" in r else "done") +
+            f" ({time.perf_counter() - t0:.1f}s)")
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -191,7 +437,17 @@ def main():
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: a 1 GiB copy (the counter calibration) and the gate/up "
                          "GEMV of every layer, then exit")
+    ap.add_argument("--workloads", default="all",
+                    help="secondary workloads measured after the decode step, comma-separated from "
+                         f"{','.join(WORKLOADS)} (default all; none: skip)")
+    ap.add_argument("--skip-decode", action="store_true",
+                    help="measure only the secondary workloads (for per-kernel profiles); prints their JSON")
     args = ap.parse_args()
+    wl_names = [] if args.workloads == "none" else list(WORKLOADS) if args.workloads == "all" else \
+        [w for w in args.workloads.split(",") if w]
+    for w in wl_names:
+        if w not in WORKLOADS:
+            ap.error(f"unknown workload {w!r}")
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not run "
               "(the multi-GPU sharding is a design note, not a measured configuration)", file=sys.stderr)
@@ -204,6 +460,9 @@ def main():
     md = import_module("a6000_custom_kernels_amd.moe_decode")
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
 
+    if args.skip_decode:
+        print(json.dumps({"workloads": run_workloads(torch, mc, md, wl_names, args)}), flush=True)
+        return
     t0 = time.perf_counter()
     fused = args.plan == "fused"
     model = md.MoeDecodeModel(torch, n_layers=args.layers, fused=fused)
@@ -292,6 +551,10 @@ def main():
                              "us_per_launch": round(dn_ms * 1000, 3), "GB/s": round(dn_gbs, 1)}},
         "cpu_baseline": cpu,
     }
+    if wl_names:
+        del model                             # 71 GiB of decode weights are not needed below
+        torch.cuda.empty_cache()
+        out["workloads"] = run_workloads(torch, mc, md, wl_names, args)
     print(json.dumps(out), flush=True)
 
 
