@@ -90,15 +90,23 @@ def down_launcher(model):
     return model.launch_down
 
 
-def traffic_probe(torch, model, md):
-    """Kernels whose per-dispatch FETCH_SIZE / WRITE_SIZE a counter run reads: three copies of
-    1 GiB (known traffic: 1 GiB read, 1 GiB written) and two gate/up GEMV launches per layer."""
+def copy_calibration(torch):
+    """Three device copies of 1 GiB (known traffic: 1 GiB read, 1 GiB written): the scale of the
+    FETCH_SIZE / WRITE_SIZE counters."""
     n = 1 << 28
     a, b = torch.empty(n, dtype=torch.float32, device="cuda"), torch.empty(n, dtype=torch.float32, device="cuda")
     a.fill_(1.0)
     torch.cuda.synchronize()
     for _ in range(3):
         b.copy_(a)
+    torch.cuda.synchronize()
+    return 4 * n
+
+
+def traffic_probe(torch, model, md):
+    """Kernels whose per-dispatch FETCH_SIZE / WRITE_SIZE a counter run reads: three copies of
+    1 GiB (known traffic: 1 GiB read, 1 GiB written) and two gate/up GEMV launches per layer."""
+    n = copy_calibration(torch) // 4
     ids_np, w_np = md.make_routing(1, model.L, model.E, model.U, seed=7)
     model.set_routing(torch.from_numpy(ids_np[0]).cuda(), torch.from_numpy(w_np[0]).cuda())
     model.launch_token()                     # builds every device table
@@ -461,6 +469,8 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
 
     if args.skip_decode:
+        if args.traffic_probe:                # counter calibration first: 1 GiB copies of known traffic
+            copy_calibration(torch)
         print(json.dumps({"workloads": run_workloads(torch, mc, md, wl_names, args)}), flush=True)
         return
     t0 = time.perf_counter()
