@@ -9,6 +9,7 @@
  */
 #include "mc_oracle.h"
 
+#include <immintrin.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -757,6 +758,122 @@ float or_vec_dot(int wt, int act_kind, int64_t k, const void *w, const void *a) 
 }
 
 /* ------------------------------------------------------------------ */
+/* AVX2 q8_K dots (the CPU baseline's vec_dot for Q2_K and Q4_K)        */
+/* ------------------------------------------------------------------ */
+
+/* The same integers or_block_isums forms per super-block, summed with 8-bit x 8-bit
+ * products (maddubs: unsigned codes x signed activations, pairs into int16, no
+ * saturation: |pair| <= 2 * 15 * 127) and int16 x int16 products (madd), then the
+ * scalar combination of or_vec_dot in the same order, so the result is bit-identical
+ * to the scalar path (ggml's generic vec_dot_q2_K_q8_K / vec_dot_q4_K_q8_K
+ * arithmetic; patches/trace-hook/ggml-cpu.c:308-340 selects q8_K for these types). */
+static int or_simd = 1;
+
+void or_set_simd(int on) { or_simd = on != 0; }
+
+static inline int32_t hsum_i32x8(__m256i v) {
+    __m128i s = _mm_add_epi32(_mm256_castsi256_si128(v), _mm256_extracti128_si256(v, 1));
+    s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0x4E));
+    s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0xB1));
+    return _mm_cvtsi128_si32(s);
+}
+
+static inline __m256i two_scales(int s0, int s1) {       /* int16 lanes 0..7 = s0, 8..15 = s1 */
+    return _mm256_set_m128i(_mm_set1_epi16((short) s1), _mm_set1_epi16((short) s0));
+}
+
+static float vec_dot_q2_K_q8_K_avx2(int64_t k, const blk_q2_K *x, const blk_q8_K *y) {
+    const int64_t nb = k / 256;
+    const __m256i m3 = _mm256_set1_epi8(3);
+    float sumf = 0.0f;
+    for (int64_t i = 0; i < nb; ++i) {
+        /* min term: sum over the 16 sub-blocks of (scales >> 4) * bsums */
+        const __m128i sc8 = _mm_loadu_si128((const __m128i *) x[i].scales);
+        const __m256i mins16 = _mm256_cvtepu8_epi16(_mm_and_si128(_mm_srli_epi16(sc8, 4), _mm_set1_epi8(0x0F)));
+        const __m256i bsums = _mm256_loadu_si256((const __m256i *) y[i].bsums);
+        const int32_t msum = hsum_i32x8(_mm256_madd_epi16(mins16, bsums));
+        /* scaled codes: element 128h + 32j + l is (qs[32h + l] >> 2j) & 3, sub-block 8h + 2j + (l >= 16) */
+        __m256i acc = _mm256_setzero_si256();
+        for (int h = 0; h < 2; ++h) {
+            const __m256i qv = _mm256_loadu_si256((const __m256i *) (x[i].qs + 32 * h));
+            for (int j = 0; j < 4; ++j) {
+                const __m256i codes = _mm256_and_si256(_mm256_srli_epi16(qv, 2 * j), m3);
+                const __m256i yv = _mm256_loadu_si256((const __m256i *) (y[i].qs + 128 * h + 32 * j));
+                const __m256i p16 = _mm256_maddubs_epi16(codes, yv);
+                const int sub = 8 * h + 2 * j;
+                acc = _mm256_add_epi32(acc, _mm256_madd_epi16(p16, two_scales(x[i].scales[sub] & 0x0F,
+                                                                                 x[i].scales[sub + 1] & 0x0F)));
+            }
+        }
+        const int32_t isum = hsum_i32x8(acc);
+        const float dall = y[i].d * H2F(x[i].d), dmin = y[i].d * H2F(x[i].dmin);
+        sumf += dall * (float) isum - dmin * (float) msum;
+    }
+    return sumf;
+}
+
+static float vec_dot_q4_K_q8_K_avx2(int64_t k, const blk_q4_K *x, const blk_q8_K *y) {
+    const int64_t nb = k / 256;
+    const __m256i m4 = _mm256_set1_epi8(0x0F);
+    float sumf = 0.0f;
+    for (int64_t i = 0; i < nb; ++i) {
+        int sc[8], m[8];
+        for (int g = 0; g < 8; ++g) scale_min_k4(g, x[i].scales, &sc[g], &m[g]);
+        /* min term: m_g * (bsums[2g] + bsums[2g+1]) */
+        const __m256i m16 = _mm256_setr_epi16((short) m[0], (short) m[0], (short) m[1], (short) m[1], (short) m[2],
+                                              (short) m[2], (short) m[3], (short) m[3], (short) m[4], (short) m[4],
+                                              (short) m[5], (short) m[5], (short) m[6], (short) m[6], (short) m[7],
+                                              (short) m[7]);
+        const __m256i bsums = _mm256_loadu_si256((const __m256i *) y[i].bsums);
+        const int32_t msum = hsum_i32x8(_mm256_madd_epi16(m16, bsums));
+        /* chunk c: low nibbles of qs[32c..] are sub-block 2c, high nibbles 2c + 1 */
+        __m256i acc = _mm256_setzero_si256();
+        for (int c = 0; c < 4; ++c) {
+            const __m256i qv = _mm256_loadu_si256((const __m256i *) (x[i].qs + 32 * c));
+            const __m256i lo = _mm256_and_si256(qv, m4), hi = _mm256_and_si256(_mm256_srli_epi16(qv, 4), m4);
+            const __m256i plo = _mm256_maddubs_epi16(lo, _mm256_loadu_si256((const __m256i *) (y[i].qs + 64 * c)));
+            const __m256i phi = _mm256_maddubs_epi16(hi, _mm256_loadu_si256((const __m256i *) (y[i].qs + 64 * c + 32)));
+            acc = _mm256_add_epi32(acc, _mm256_madd_epi16(plo, _mm256_set1_epi16((short) sc[2 * c])));
+            acc = _mm256_add_epi32(acc, _mm256_madd_epi16(phi, _mm256_set1_epi16((short) sc[2 * c + 1])));
+        }
+        const int32_t isum = hsum_i32x8(acc);
+        const float dall = y[i].d * H2F(x[i].d), dmin = y[i].d * H2F(x[i].dmin);
+        sumf += dall * (float) isum - dmin * (float) msum;
+    }
+    return sumf;
+}
+
+/* Q4_0 x q8_0: per 32-value block, sum((code - 8) * q8) = sum(code * q8) - 8 * sum(q8), both exact
+ * integer sums, combined as (float) isum * d_w * d_a like the scalar path. */
+static float vec_dot_q4_0_q8_0_avx2(int64_t k, const blk_q4_0 *x, const blk_q8_0 *y) {
+    const int64_t nb = k / 32;
+    const __m128i m4 = _mm_set1_epi8(0x0F);
+    const __m256i ones8 = _mm256_set1_epi8(1);
+    const __m256i ones16 = _mm256_set1_epi16(1);
+    float sumf = 0.0f;
+    for (int64_t i = 0; i < nb; ++i) {
+        const __m128i q = _mm_loadu_si128((const __m128i *) x[i].qs);
+        /* codes of values 0..15 (low nibbles) then 16..31 (high nibbles) */
+        const __m256i codes = _mm256_set_m128i(_mm_and_si128(_mm_srli_epi16(q, 4), m4), _mm_and_si128(q, m4));
+        const __m256i yv = _mm256_loadu_si256((const __m256i *) y[i].qs);
+        const int32_t cy = hsum_i32x8(_mm256_madd_epi16(_mm256_maddubs_epi16(codes, yv), ones16));
+        const int32_t sy = hsum_i32x8(_mm256_madd_epi16(_mm256_maddubs_epi16(ones8, yv), ones16));
+        const int32_t isum = cy - 8 * sy;
+        sumf += (float) isum * H2F(x[i].d) * H2F(y[i].d);
+    }
+    return sumf;
+}
+
+/* ggml-CPU vec_dot (q8_0 / q8_K activations): AVX2 for Q4_0, Q2_K and Q4_K when enabled,
+ * the scalar restatement otherwise. */
+float or_vec_dot_cpu(int wt, int64_t k, const void *w, const void *a) {
+    if (or_simd && wt == OR_Q4_0) return vec_dot_q4_0_q8_0_avx2(k, (const blk_q4_0 *) w, (const blk_q8_0 *) a);
+    if (or_simd && wt == OR_Q2_K) return vec_dot_q2_K_q8_K_avx2(k, (const blk_q2_K *) w, (const blk_q8_K *) a);
+    if (or_simd && wt == OR_Q4_K) return vec_dot_q4_K_q8_K_avx2(k, (const blk_q4_K *) w, (const blk_q8_K *) a);
+    return or_vec_dot(wt, OR_ACT_CPU, k, w, a);
+}
+
+/* ------------------------------------------------------------------ */
 /* GLU                                                                 */
 /* ------------------------------------------------------------------ */
 
@@ -930,7 +1047,7 @@ int or_cpu_mul_mat_id_f32(int type, int64_t ne00, int64_t ne01, int32_t n_as,
                 const int32_t c = m[0], t = m[1];
                 const char *a = wdata + (size_t) ((c % ne11) + (int64_t) t * ne11) * arb;
                 float *d = dst + (int64_t) t * dst_stride_col + (int64_t) c * dst_stride_channel;
-                for (int64_t r = r0s; r < r0e; ++r) d[r] = or_vec_dot(type, OR_ACT_CPU, ne00, w + (size_t) r * nb01, a);
+                for (int64_t r = r0s; r < r0e; ++r) d[r] = or_vec_dot_cpu(type, ne00, w + (size_t) r * nb01, a);
             }
         }
     }

@@ -84,6 +84,10 @@ void   or_quantize_act_row(int wtype, int act_kind, const float *x, void *y, int
 
 /* Dot of one weight row (k elements of `wtype`) with one activation row. */
 float or_vec_dot(int wtype, int act_kind, int64_t k, const void *w, const void *a);
+/* ggml-CPU vec_dot with q8_0 / q8_K activations: AVX2 for Q2_K and Q4_K (bit-identical
+ * to or_vec_dot's scalar path) unless or_set_simd(0), scalar otherwise. */
+float or_vec_dot_cpu(int wtype, int64_t k, const void *w, const void *a);
+void or_set_simd(int on);
 
 /* Exact integer partial sums of one block (for bit-exact checks):
  * out[j] for the block's sub-blocks, as documented in mc_oracle.c. */

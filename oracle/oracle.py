@@ -73,6 +73,8 @@ def lib():
         L.or_act_row_bytes.argtypes, L.or_act_row_bytes.restype = [C.c_int, C.c_int, i64], sz
         L.or_quantize_act_row.argtypes, L.or_quantize_act_row.restype = [C.c_int, C.c_int, vp, vp, i64], None
         L.or_vec_dot.argtypes, L.or_vec_dot.restype = [C.c_int, C.c_int, i64, vp, vp], C.c_float
+        L.or_vec_dot_cpu.argtypes, L.or_vec_dot_cpu.restype = [C.c_int, i64, vp, vp], C.c_float
+        L.or_set_simd.argtypes, L.or_set_simd.restype = [C.c_int], None
         L.or_block_isums.argtypes, L.or_block_isums.restype = [C.c_int, vp, vp, vp], C.c_int
         L.or_glu.argtypes, L.or_glu.restype = [C.c_int, C.c_float, C.c_float, C.c_float], C.c_float
         L.or_mul_mat_id.argtypes, L.or_mul_mat_id.restype = [C.POINTER(_MmidArgs)], C.c_int
@@ -187,6 +189,17 @@ def vec_dot(wtype, act_kind, k, wrow, arow):
     wrow = np.ascontiguousarray(wrow, dtype=np.uint8)
     arow = np.ascontiguousarray(arow, dtype=np.uint8)
     return lib().or_vec_dot(wtype, act_kind, k, wrow.ctypes.data, arow.ctypes.data)
+
+
+def vec_dot_cpu(wtype, k, wrow, arow):
+    """ggml-CPU vec_dot (q8_0 / q8_K activation row): AVX2 for Q2_K / Q4_K unless set_simd(False)."""
+    wrow, arow = np.ascontiguousarray(wrow), np.ascontiguousarray(arow)
+    return lib().or_vec_dot_cpu(wtype, k, wrow.ctypes.data, arow.ctypes.data)
+
+
+def set_simd(on: bool):
+    """AVX2 q8_K dots in the ggml-CPU MUL_MAT_ID restatement (default on) or the scalar path."""
+    lib().or_set_simd(1 if on else 0)
 
 
 def block_isums(wtype, wblock, q8):

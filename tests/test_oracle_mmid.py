@@ -109,3 +109,47 @@ def test_combine_against_numpy():
     for c in chunks:
         total = np.float32(total + np.float32(c))
     assert O.rms_sum(xt) == total
+
+
+@pytest.mark.parametrize("wtype", [2, 10, 12])
+def test_avx2_vec_dot_bit_identical_to_scalar(O, wtype):
+    """The AVX2 Q2_K / Q4_K x q8_K dots (the CPU baseline's) equal the scalar restatement bit for bit: same
+    per-super-block integers, same fp32 combination order.  Random blocks (every code and scale value),
+    extreme activations (+-127 everywhere) and a zero row."""
+    rng = np.random.default_rng(wtype)
+    K = 4096
+    rb = O.row_bytes(wtype, K)
+    for trial in range(40):
+        w = rng.integers(0, 256, rb, dtype=np.uint8)
+        # finite fp16 block scales
+        bb = O.block_bytes(wtype)
+        for off in ((80, 82) if wtype == 10 else (0, 2) if wtype == 12 else (0,)):
+            for b in range(K // O.block_elems(wtype)):
+                h = np.array([rng.uniform(-0.05, 0.05)], np.float16).view(np.uint8)
+                w[b * bb + off:b * bb + off + 2] = h
+        if trial == 0:
+            x = np.full(K, 3.0, np.float32)
+        elif trial == 1:
+            x = np.zeros(K, np.float32)
+        else:
+            x = rng.standard_normal(K).astype(np.float32) * (10.0 ** rng.uniform(-3, 3))
+        a = O.quantize_q8_K(x) if wtype != 2 else O.quantize_q8_0(x)
+        O.set_simd(False)
+        ref = O.vec_dot_cpu(wtype, K, w, a)
+        O.set_simd(True)
+        got = O.vec_dot_cpu(wtype, K, w, a)
+        assert np.float32(got).view(np.uint32) == np.float32(ref).view(np.uint32), (trial, got, ref)
+        assert np.float32(ref).view(np.uint32) == np.float32(O.vec_dot(wtype, O.ACT_CPU, K, w, a)).view(np.uint32)
+
+
+def test_cpu_mul_mat_id_simd_equals_scalar(O):
+    import helpers as H
+    for wtype in (2, 10, 12):
+        w = H.weights(wtype, 8, 64, 2048, seed=5 + wtype)
+        x = H.activations(3, 2048, seed=6)
+        ids = H.routing(3, 4, 8, seed=7)
+        O.set_simd(False)
+        ref = O.cpu_mul_mat_id_f32(wtype=wtype, K=2048, R=64, n_as=8, src0=w, src1=x, ids=ids)
+        O.set_simd(True)
+        got = O.cpu_mul_mat_id_f32(wtype=wtype, K=2048, R=64, n_as=8, src0=w, src1=x, ids=ids)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
