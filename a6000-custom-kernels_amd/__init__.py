@@ -29,6 +29,8 @@ TYPE_NAMES = {Q4_0: "q4_0", Q5_0: "q5_0", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_
 GLU_REGLU, GLU_GEGLU, GLU_SWIGLU, GLU_SWIGLU_OAI, GLU_GEGLU_ERF, GLU_GEGLU_QUICK, GLU_SWIGLU_CLAMP = range(7)
 # activation formats
 ACT_Q8_1, ACT_Q8_K, ACT_F32 = 0, 1, 2
+# graph node ops for fusion detection
+OP_MUL_MAT, OP_MUL_MAT_ID, OP_ADD_ID, OP_MUL, OP_ADD, OP_GLU, OP_OTHER = range(1, 8)
 
 MISS_CAP = 8190
 STATS_WORDS = 2 + MISS_CAP
@@ -53,6 +55,12 @@ class Fusion(C.Structure):
                 ("glu_limit", C.c_float), ("shared_up", C.c_void_p), ("shared_gate", C.c_void_p),
                 ("shared_dst", C.c_void_p), ("shared_stride_col_dst", C.c_int64), ("shared_type", C.c_int32),
                 ("shared_src1", C.c_void_p), ("shared_stride_col_y", C.c_int64), ("bias_stride", C.c_int64)]
+
+
+class Node(C.Structure):
+    """ggml_hip_moe_node: one graph node (op, result tensor, node-index or leaf sources)."""
+    _fields_ = [("op", C.c_int32), ("t", Tensor), ("src", C.c_int32 * 3), ("leaf", Tensor * 3),
+                ("glu_op", C.c_int32), ("glu_limit", C.c_float), ("glu_swapped", C.c_int32)]
 
 
 class Config(C.Structure):
@@ -119,6 +127,9 @@ SIGNATURES = [
       C.POINTER(Fusion), _VP, _I64, _VP]),
     ("ggml_hip_moe_mul_mat_id_noalloc", C.c_int,
      [C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Fusion), _VP]),
+    ("ggml_hip_moe_fusion_detect", C.c_int,
+     [C.POINTER(Node), _I32, _I32, C.POINTER(Fusion), C.POINTER(Tensor), C.POINTER(_I32), C.POINTER(_I32),
+      C.POINTER(_I32)]),
     ("ggml_hip_ssm_conv_f32", C.c_int,
      [_VP, _I64, _I64, _I64, _VP, C.c_int32, _I64, _VP, C.c_int32, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
       _VP]),
@@ -399,6 +410,26 @@ def mul_mat_id(*, wtype, weights, x, ids, dst, K, R, n_experts, fusion=None, wor
                                        workspace.data_ptr(), workspace.numel(), _stream(stream))
     check(rc, "mul_mat_id")
     return dst
+
+
+def fusion_detect(nodes, i_up, library=None):
+    """Graph-level fusion detection through ggml_hip_moe_fusion_detect.
+
+    nodes: a sequence of Node.  Returns (n_covered, fusion, gate_host or None, covered flags, out_node).
+    """
+    L = library if library is not None else lib()
+    n = len(nodes)
+    arr = (Node * n)(*nodes)
+    f = Fusion()
+    gh = Tensor()
+    has_gh = C.c_int32(0)
+    covered = (C.c_int32 * n)()
+    out_node = C.c_int32(-1)
+    rc = L.ggml_hip_moe_fusion_detect(arr, n, i_up, C.byref(f), C.byref(gh), C.byref(has_gh), covered,
+                                      C.byref(out_node))
+    if rc < 0:
+        raise MoeError("fusion_detect: " + L.ggml_hip_moe_last_error().decode(errors="replace"))
+    return rc, f, (gh if has_gh.value else None), [bool(c) for c in covered], out_node.value
 
 
 def ssm_conv(x, w, *, bias=None, silu=False, out=None, n_t=None, stream=None):

@@ -787,6 +787,79 @@ int mmid_run(const MmidPlan &p, const ggml_hip_moe_tensor *src0, const ggml_hip_
                        sch_dst, ids_stride, stream, nullptr, no_tables);
 }
 
+
+// ---------------------------------------------------------------------------
+// graph-level fusion detection (the decision ggml-cuda makes before the
+// intercept, patches/apply_patches.py:42-62; consumed at kernels/moe-cache.cu:109-129)
+// ---------------------------------------------------------------------------
+
+constexpr int OP_MUL_MAT = 1, OP_MUL_MAT_ID = 2, OP_ADD_ID = 3, OP_MUL = 4, OP_GLU = 6;
+
+struct Graph {
+    const ggml_hip_moe_node *n;
+    int count;
+    std::vector<int> uses;              // consumers of each node
+    std::vector<int> sole;              // the only consumer, or -1
+
+    Graph(const ggml_hip_moe_node *nodes, int cnt) : n(nodes), count(cnt), uses(cnt, 0), sole(cnt, -1) {
+        for (int k = 0; k < cnt; ++k)
+            for (int s = 0; s < 3; ++s) {
+                const int j = nodes[k].src[s];
+                if (j >= 0 && j < cnt && j != k) {
+                    uses[j] += 1;
+                    sole[j] = uses[j] == 1 ? k : -1;
+                }
+            }
+    }
+    // the same source: one node, or leaves over the same memory and shape
+    bool same_src(int a, int sa, int b, int sb) const {
+        const int ia = n[a].src[sa], ib = n[b].src[sb];
+        if (ia >= 0 || ib >= 0) return ia == ib;
+        const ggml_hip_moe_tensor &x = n[a].leaf[sa], &y = n[b].leaf[sb];
+        return x.data == y.data && x.type == y.type && !memcmp(x.ne, y.ne, sizeof(x.ne)) && !memcmp(x.nb, y.nb, sizeof(x.nb));
+    }
+    // data pointer of a node's source (node result or leaf)
+    const ggml_hip_moe_tensor &src_tensor(int k, int s) const {
+        const int j = n[k].src[s];
+        return j >= 0 ? n[j].t : n[k].leaf[s];
+    }
+};
+
+// Follows an expert path from MUL_MAT_ID node `mm`: an optional MUL by a per-expert scale leaf
+// with the same ids, then an optional ADD_ID by a per-expert bias leaf with the same ids -- the
+// order in which the kernels apply them (kernels/moe-cache.cu:246-252, :257-262).  Returns the
+// path's last node; bias / scale receive the leaves' data.
+int follow_expert_path(const Graph &g, int mm, const float **bias, int64_t *bias_stride, const float **scale,
+                       std::vector<int> &path) {
+    int cur = mm;
+    path.push_back(cur);
+    const ggml_hip_moe_node &m = g.n[mm];
+    const int64_t rows = m.t.ne[0];
+    const int64_t n_exp = g.src_tensor(mm, 0).ne[2];
+    int nxt = g.sole[cur];
+    if (nxt >= 0 && g.n[nxt].op == OP_MUL && g.n[nxt].src[0] == cur && g.n[nxt].src[1] < 0 &&
+        g.same_src(nxt, 2, mm, 2)) {
+        const ggml_hip_moe_tensor &sc = g.n[nxt].leaf[1];
+        if (sc.type == 0 && sc.ne[0] == 1 && sc.ne[1] == n_exp && sc.nb[1] == 4) {
+            *scale = (const float *) sc.data;
+            cur = nxt;
+            path.push_back(cur);
+            nxt = g.sole[cur];
+        }
+    }
+    if (nxt >= 0 && g.n[nxt].op == OP_ADD_ID && g.n[nxt].src[0] == cur && g.n[nxt].src[1] < 0 &&
+        g.same_src(nxt, 2, mm, 2)) {
+        const ggml_hip_moe_tensor &b = g.n[nxt].leaf[1];
+        if (b.type == 0 && b.ne[0] == rows && b.ne[1] == n_exp && b.nb[0] == 4 && b.nb[1] % 4 == 0) {
+            *bias = (const float *) b.data;
+            *bias_stride = (int64_t) (b.nb[1] / 4);
+            cur = nxt;
+            path.push_back(cur);
+        }
+    }
+    return cur;
+}
+
 // routing trace files opened by ggml_hip_moe_trace_append: path -> append stream
 std::mutex g_trace_mutex;
 std::unordered_map<std::string, FILE *> g_trace_files;
@@ -1374,6 +1447,139 @@ int ggml_hip_moe_trace_close(void) {
         if (kv.second && fclose(kv.second) != 0 && !rc) rc = fail(E_INVALID, "trace_close: %s", kv.first.c_str());
     g_trace_files.clear();
     return rc;
+}
+
+int ggml_hip_moe_fusion_detect(const ggml_hip_moe_node *nodes, int32_t n_nodes, int32_t i_up, ggml_hip_moe_fusion *fusion,
+                               ggml_hip_moe_tensor *gate_host, int32_t *has_gate_host, int32_t *covered, int32_t *out_node) {
+    if (!nodes || n_nodes <= 0 || !fusion || !gate_host || !has_gate_host || !covered || !out_node)
+        return fail(E_INVALID, "fusion_detect: null argument");
+    if (i_up < 0 || i_up >= n_nodes || nodes[i_up].op != OP_MUL_MAT_ID)
+        return fail(E_INVALID, "fusion_detect: node %d is not a MUL_MAT_ID", i_up);
+    for (int k = 0; k < n_nodes; ++k)
+        for (int s = 0; s < 3; ++s)
+            if (nodes[k].src[s] >= n_nodes) return fail(E_INVALID, "fusion_detect: node %d source %d out of range", k, s);
+    const Graph g(nodes, n_nodes);
+    memset(fusion, 0, sizeof(*fusion));
+    memset(gate_host, 0, sizeof(*gate_host));
+    for (int k = 0; k < n_nodes; ++k) covered[k] = 0;
+    fusion->glu_op = GGML_HIP_MOE_GLU_SWIGLU;
+    fusion->shared_type = -1;
+    *has_gate_host = 0;
+    *out_node = i_up;
+    covered[i_up] = 1;
+
+    // up path, then the GLU that consumes it
+    std::vector<int> up_path;
+    const float *x_bias = nullptr, *x_scale = nullptr;
+    int64_t x_bias_stride = 0;
+    const int up_end = follow_expert_path(g, i_up, &x_bias, &x_bias_stride, &x_scale, up_path);
+    const int glu = g.sole[up_end];
+    int gate_mm = -1, gate_end = -1;
+    std::vector<int> gate_path;
+    const float *g_bias = nullptr, *g_scale = nullptr;
+    int64_t g_bias_stride = 0;
+    if (glu >= 0 && nodes[glu].op == OP_GLU) {
+        const bool sw = nodes[glu].glu_swapped != 0;
+        const int up_slot = sw ? 0 : 1, gate_slot = sw ? 1 : 0;
+        if (nodes[glu].src[up_slot] == up_end) {
+            // the gate operand must be the end of a matching gate MUL_MAT_ID path
+            const int ge = nodes[glu].src[gate_slot];
+            int cand = ge;
+            // walk back through at most an ADD_ID and a MUL to the gate MUL_MAT_ID
+            for (int hop = 0; hop < 2 && cand >= 0 && nodes[cand].op != OP_MUL_MAT_ID; ++hop) cand = nodes[cand].src[0];
+            if (cand >= 0 && cand != i_up && nodes[cand].op == OP_MUL_MAT_ID && g.same_src(cand, 1, i_up, 1) &&
+                g.same_src(cand, 2, i_up, 2)) {
+                const ggml_hip_moe_tensor &wu = g.src_tensor(i_up, 0), &wg = g.src_tensor(cand, 0);
+                const bool same_shape = wu.type == wg.type && !memcmp(wu.ne, wg.ne, sizeof(wu.ne)) && wu.nb[2] == wg.nb[2] &&
+                                        wu.nb[1] == wg.nb[1];
+                if (same_shape && g.uses[cand] == 1) {
+                    gate_end = follow_expert_path(g, cand, &g_bias, &g_bias_stride, &g_scale, gate_path);
+                    if (gate_end == ge) gate_mm = cand;
+                }
+            }
+        }
+        // every absorbed intermediate feeds only the next node of its path
+        bool ok = gate_mm >= 0;
+        for (size_t k = 0; ok && k + 1 < up_path.size(); ++k) ok = g.sole[up_path[k]] == up_path[k + 1];
+        for (size_t k = 0; ok && k + 1 < gate_path.size(); ++k) ok = g.sole[gate_path[k]] == gate_path[k + 1];
+        ok = ok && g.sole[up_end] == glu && g.sole[gate_end] == glu;
+        if (x_bias && g_bias && x_bias_stride != g_bias_stride) ok = false;
+        const int op = ok ? nodes[glu].glu_op : -1;
+        if (op < GGML_HIP_MOE_GLU_REGLU || op > GGML_HIP_MOE_GLU_SWIGLU_CLAMP) ok = false;
+        // the gate goes to the kernel as a host tensor for the cache path (registered with its own
+        // table when host-resident), else as device memory that the kernel reads directly
+        const bool cache_up = ok && wants_impl(&g.src_tensor(i_up, 0));
+        if (ok && !cache_up && ptr_kind_cached(g.src_tensor(gate_mm, 0).data) != PTR_DEVICE) ok = false;
+        if (ok) {
+            fusion->glu_op = op;
+            fusion->glu_limit = nodes[glu].glu_limit;
+            fusion->x_bias = x_bias;
+            fusion->x_scale = x_scale;
+            fusion->gate_bias = g_bias;
+            fusion->gate_scale = g_scale;
+            fusion->bias_stride = x_bias ? x_bias_stride : g_bias_stride;
+            if (cache_up) {
+                *gate_host = g.src_tensor(gate_mm, 0);
+                *has_gate_host = 1;
+            } else {
+                fusion->gate = g.src_tensor(gate_mm, 0).data;
+            }
+            for (int k : up_path) covered[k] = 1;
+            for (int k : gate_path) covered[k] = 1;
+            covered[glu] = 1;
+            *out_node = glu;
+        }
+    }
+    if (*out_node == i_up) {
+        // no gate: the up path's bias and scale alone still fuse into the plain GEMV
+        bool ok = true;
+        for (size_t k = 0; ok && k + 1 < up_path.size(); ++k) ok = g.sole[up_path[k]] == up_path[k + 1];
+        if (ok && up_path.size() > 1) {
+            fusion->x_bias = x_bias;
+            fusion->x_scale = x_scale;
+            fusion->bias_stride = x_bias_stride;
+            for (int k : up_path) covered[k] = 1;
+            *out_node = up_end;
+        }
+    }
+
+    // shared expert on the same activations: MUL_MAT(sh_up, x), MUL_MAT(sh_gate, x), GLU(sh_gate, sh_up)
+    const bool routed_glu = *out_node != i_up && nodes[*out_node].op == OP_GLU;
+    {
+        const ggml_hip_moe_tensor &x = g.src_tensor(i_up, 1);
+        const int64_t rows = nodes[i_up].t.ne[0], K = g.src_tensor(i_up, 0).ne[0];
+        for (int k = 0; k < n_nodes; ++k) {
+            if (nodes[k].op != OP_GLU || covered[k]) continue;
+            const bool sw = nodes[k].glu_swapped != 0;
+            const int su = nodes[k].src[sw ? 0 : 1], sg = nodes[k].src[sw ? 1 : 0];
+            if (su < 0 || sg < 0 || nodes[su].op != OP_MUL_MAT || nodes[sg].op != OP_MUL_MAT) continue;
+            if (g.uses[su] != 1 || g.uses[sg] != 1) continue;
+            const ggml_hip_moe_tensor &xu = g.src_tensor(su, 1), &xg = g.src_tensor(sg, 1);
+            if (xu.data != x.data || xg.data != x.data) continue;     // the routed experts' input rows
+            const ggml_hip_moe_tensor &wu = g.src_tensor(su, 0), &wg = g.src_tensor(sg, 0);
+            if (wu.type != wg.type || !type_supported(wu.type) || wu.ne[0] != K || wu.ne[1] != rows ||
+                memcmp(wu.ne, wg.ne, sizeof(wu.ne)) || wu.ne[2] != 1)
+                continue;
+            if (routed_glu && nodes[k].glu_op != fusion->glu_op) continue;          // one GLU op per launch
+            if (ptr_kind_cached(wu.data) != PTR_DEVICE || ptr_kind_cached(wg.data) != PTR_DEVICE) continue;
+            const ggml_hip_moe_tensor &out = nodes[k].t;
+            if (out.type != 0 || out.nb[0] != 4 || out.nb[1] % 4) continue;
+            fusion->shared_up = wu.data;
+            fusion->shared_gate = wg.data;
+            fusion->shared_type = wu.type;
+            fusion->shared_dst = (float *) out.data;
+            fusion->shared_stride_col_dst = (int64_t) (out.nb[1] / 4);
+            if (!routed_glu) {
+                fusion->glu_op = nodes[k].glu_op;
+                fusion->glu_limit = nodes[k].glu_limit;
+            }
+            covered[su] = covered[sg] = covered[k] = 1;
+            break;
+        }
+    }
+    int n = 0;
+    for (int k = 0; k < n_nodes; ++k) n += covered[k];
+    return n;
 }
 
 int ggml_hip_moe_check_status(void *stream) {

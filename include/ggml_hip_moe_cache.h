@@ -410,6 +410,57 @@ int ggml_hip_moe_mul_mat_id_noalloc(const ggml_hip_moe_tensor *src0, const ggml_
                                     const ggml_hip_moe_fusion *fusion, void *stream);
 
 /* ---------------------------------------------------------------------
+ * Graph-level fusion detection: the decision ggml-cuda's graph evaluator makes
+ * before the reference's intercept (patches/apply_patches.py:42-62,
+ * results/final.patch:66-82), producing the fusion arguments the intercept
+ * consumes (kernels/moe-cache.cu:109-129).  The caller mirrors the nodes of a
+ * MoE FFN block (ggml's op, sources and result tensor) into an array.
+ * --------------------------------------------------------------------- */
+
+enum {
+    GGML_HIP_MOE_OP_MUL_MAT    = 1,   /* dst = src0 (weights) x src1 */
+    GGML_HIP_MOE_OP_MUL_MAT_ID = 2,   /* src0 experts, src1 activations, src2 ids */
+    GGML_HIP_MOE_OP_ADD_ID     = 3,   /* dst = src0 + src1[:, src2 (ids)] (per-expert bias rows) */
+    GGML_HIP_MOE_OP_MUL        = 4,   /* dst = src0 * src1 */
+    GGML_HIP_MOE_OP_ADD        = 5,   /* dst = src0 + src1 */
+    GGML_HIP_MOE_OP_GLU        = 6,   /* dst = glu_op(src0, src1); swapped: the roles of src0 and src1 exchanged */
+    GGML_HIP_MOE_OP_OTHER      = 7
+};
+
+/* One graph node: its op, its result tensor, and for each source either the index of
+ * the producing node in the same array (src[k] >= 0) or a leaf tensor (src[k] < 0:
+ * leaf[k], e.g. weights, biases, the ids, an input computed elsewhere).  A MUL by a
+ * per-expert scale has a leaf src1 of ne [1, n_experts] and src2 = the ids (ggml's
+ * get_rows of the scale by the ids, folded into the node). */
+typedef struct ggml_hip_moe_node {
+    int32_t             op;
+    ggml_hip_moe_tensor t;
+    int32_t             src[3];
+    ggml_hip_moe_tensor leaf[3];
+    int32_t             glu_op;       /* GLU: GGML_HIP_MOE_GLU_* */
+    float               glu_limit;    /* GLU: SWIGLU_CLAMP limit */
+    int32_t             glu_swapped;  /* GLU: 1 when src0 is the up (value) operand and src1 the gate */
+} ggml_hip_moe_node;
+
+/* For the MUL_MAT_ID node i_up, the largest fusable pattern around it:
+ *   up path    MUL_MAT_ID(w_up, x, ids) [-> MUL(x_scale, ids)] [-> ADD_ID(x_bias, ids)]
+ *   gate path  MUL_MAT_ID(w_gate, x, ids) [-> MUL(gate_scale, ids)] [-> ADD_ID(gate_bias, ids)]
+ *   GLU(gate path, up path)
+ *   shared     MUL_MAT(sh_up, x), MUL_MAT(sh_gate, x), GLU(sh_gate, sh_up) on the same x
+ * Every absorbed intermediate must have the next node as its only consumer, the gate
+ * MUL_MAT_ID must match the up one (type, shape, activations, ids), and the GLU ops must
+ * agree.  Fills *fusion (glu_op, biases, scales, shared_* with shared_dst = the shared
+ * GLU's tensor; gate = the gate's data when the cache does not want w_up) and
+ * *gate_host (the gate weights, for the cache path; *has_gate_host = 0 when none),
+ * sets covered[k] = 1 for every node the fused call computes (covered has n_nodes
+ * entries) and *out_node to the node whose tensor receives the result.  Returns the
+ * number of covered nodes (1: nothing fused, a plain MUL_MAT_ID), or < 0 when node
+ * i_up is not a MUL_MAT_ID or the array is malformed. */
+int ggml_hip_moe_fusion_detect(const ggml_hip_moe_node *nodes, int32_t n_nodes, int32_t i_up,
+                               ggml_hip_moe_fusion *fusion, ggml_hip_moe_tensor *gate_host,
+                               int32_t *has_gate_host, int32_t *covered, int32_t *out_node);
+
+/* ---------------------------------------------------------------------
  * SSM_CONV with F32 or F16 conv weights (kernels/ssm-conv.cu:117-217: the
  * reference's ssm_conv_f32_cuda / ggml_cuda_op_ssm_conv, templated on the
  * weight type so that F16 conv1d weights work; the fused ADD(bias) + SiLU).

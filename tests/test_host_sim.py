@@ -11,30 +11,7 @@ import cache_scenario as S
 from oracle.cache_model import CacheModel
 
 ROOT = Path(__file__).resolve().parent.parent
-SIM = ROOT / "tests" / "native" / "_build" / "libmc_hostsim.so"
 SEED_FIXTURE = ROOT / "tests" / "golden" / "moe_seed.txt"
-
-
-@pytest.fixture(scope="module")
-def sim(mc):
-    srcs = [ROOT / "a6000-custom-kernels_amd" / "csrc" / "mc_host.cpp", ROOT / "tests" / "native" / "sim_device.cpp",
-            ROOT / "include" / "ggml_hip_moe_cache.h"]
-    if not SIM.exists() or max(p.stat().st_mtime for p in srcs) > SIM.stat().st_mtime:
-        import importlib.util
-        spec = importlib.util.spec_from_file_location("mc_build", ROOT / "a6000-custom-kernels_amd" / "build.py")
-        b = importlib.util.module_from_spec(spec)
-        spec.loader.exec_module(b)
-        b.build_hostsim()
-    lib = mc.bind(SIM)
-    lib.mc_sim_host_alloc.restype, lib.mc_sim_host_alloc.argtypes = C.c_void_p, [C.c_uint64]
-    lib.mc_sim_plain_alloc.restype, lib.mc_sim_plain_alloc.argtypes = C.c_void_p, [C.c_uint64]
-    lib.mc_sim_dev_alloc.restype, lib.mc_sim_dev_alloc.argtypes = C.c_void_p, [C.c_uint64]
-    lib.mc_sim_set_mem_info.argtypes = [C.c_uint64, C.c_uint64]
-    lib.mc_sim_fail_alloc_after.argtypes = [C.c_int]
-    lib.mc_sim_fail_h2d_after.argtypes = [C.c_int]
-    lib.mc_sim_live_regions.restype = C.c_longlong
-    lib.mc_sim_counters.argtypes = [C.c_void_p]
-    return lib
 
 
 class SimBackend:
