@@ -29,6 +29,7 @@ TYPE_NAMES = {Q4_0: "q4_0", Q5_0: "q5_0", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_
 GLU_REGLU, GLU_GEGLU, GLU_SWIGLU, GLU_SWIGLU_OAI, GLU_GEGLU_ERF, GLU_GEGLU_QUICK, GLU_SWIGLU_CLAMP = range(7)
 # activation formats
 ACT_Q8_1, ACT_Q8_K, ACT_F32 = 0, 1, 2
+ACT_SHARED_F32 = 0x100       # ffn_down_combine flag: the shared expert's rows are fp32
 # graph node ops for fusion detection
 OP_MUL_MAT, OP_MUL_MAT_ID, OP_ADD_ID, OP_MUL, OP_ADD, OP_GLU, OP_OTHER = range(1, 8)
 
@@ -326,7 +327,7 @@ def ffn_down_combine(*, wtype, weights, ids, h, router_w, x_out, K, R, n_experts
     keep = []
     ptr = weights_ptr if weights_ptr is not None else weights.data_ptr()
     src0 = make_tensor(wtype, K, R, n_experts, ptr, name=name, keep=keep)
-    unit = 1 if act == ACT_F32 else 36          # h strides in floats or in q8_1 blocks
+    unit = 1 if (act & 0xFF) == ACT_F32 else 36   # h strides in floats or in q8_1 blocks
     rc = lib().ggml_hip_moe_ffn_down_combine(
         1 if use_cache else 0, act, C.byref(src0), C.byref(fusion) if fusion is not None else None, h.data_ptr(),
         ids.data_ptr(), router_w.data_ptr(), _ptr(residual), x_out.data_ptr(), K, R, n_experts, n_tok, n_used,

@@ -727,6 +727,25 @@ __device__ __forceinline__ float step_row_sum(float *red, float v, int nu) {
     return s;
 }
 
+// q8 codes roundf(v / d) of values |v| <= amax, d = amax / 127 (IEEE), with one IEEE
+// reciprocal per block instead of a division per value.  For a normal, finite d the
+// product y = v * fl(1/d) is within 2^-15 of fl(v / d): |v / d| <= 127 + 2^-16, the two
+// roundings of the product add at most 2^-16 and fl(v / d) itself at most 2^-18.  So
+// wherever y lies at least 2^-14 away from a half-integer, rint(y) == roundf(fl(v / d)).
+// The remaining values, and every value of a block whose d is zero, subnormal or not
+// finite, are flagged (slow) for the division.
+__device__ __forceinline__ bool q8_scale_ok(float d) { return d >= 0x1p-126f && d <= 0x1.fffffep+127f; }
+
+__device__ __forceinline__ int q8_code_fast(float v, float inv, bool d_ok, bool &slow) {
+    const float y = v * (d_ok ? inv : 0.0f);
+    const float r = __builtin_rintf(y);
+    slow = !d_ok || fabsf(y - r) >= 0.5f - 0x1p-14f;
+    return (int) r;
+}
+
+// The division of the flagged values (d = 0 divides by 1; the caller writes 0 for it).
+__device__ __forceinline__ int q8_code_exact(float v, float d) { return (int) roundf(v / (d != 0.0f ? d : 1.0f)); }
+
 // q8_1 quantization of one 32-value block spread over a 32-lane half-wave (the
 // arithmetic of ggml-CUDA quantize_q8_1): amax over the half-wave, d = amax/127
 // (IEEE division), q = amax == 0 ? 0 : roundf(x/d).  Also returns the xor-butterfly sum.
@@ -739,7 +758,13 @@ __device__ __forceinline__ int8_t q8_1_lane(float x, float &d, float &sum) {
         sum += xor_lanes_rt(sum, off);
     }
     d = amax / 127.0f;
-    return amax == 0.0f ? (int8_t) 0 : (int8_t) roundf(x / d);
+    const bool dok = q8_scale_ok(d);
+    bool slow;
+    int q = q8_code_fast(x, 1.0f / (dok ? d : 1.0f), dok, slow);
+    if (__builtin_amdgcn_ballot_w64(slow) != 0) {            // rare: see q8_code_fast
+        if (slow) q = q8_code_exact(x, d);
+    }
+    return amax == 0.0f ? (int8_t) 0 : (int8_t) q;
 }
 
 // q8_1 blocks of the k fp32 values at x (LDS, 4-byte aligned, k % 32 == 0) into
@@ -775,13 +800,28 @@ __device__ __forceinline__ void quantize_row_lds(const float *x, uint8_t *q, int
         for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
         amax = fmaxf(amax, xor_lanes<1>(amax));              // the partner lane of the block
         const float d = amax / 127.0f;
+        const bool dok = q8_scale_ok(d);
+        const float inv = 1.0f / (dok ? d : 1.0f);
+        int qv[16];
+        u32 slow = 0u;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            bool sl;
+            qv[i] = q8_code_fast(v[i], inv, dok, sl);
+            slow |= (sl ? 1u : 0u) << i;
+        }
+        if (__builtin_amdgcn_ballot_w64(slow != 0u) != 0) {  // rare: see q8_code_fast
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (slow & (1u << i)) qv[i] = q8_code_exact(v[i], d);
+        }
         u32 packed[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             u32 wd = 0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int code = amax == 0.0f ? 0 : (int) roundf(v[4 * i + j] / d);
+                const int code = amax == 0.0f ? 0 : qv[4 * i + j];
                 wd |= ((u32) code & 0xFFu) << (8 * j);
             }
             packed[i] = wd;
@@ -902,14 +942,25 @@ __device__ __forceinline__ void quantize_chunk(const float xv[4], bool norm, flo
         sum = t2[0] + t2[1];
     }
     const float d = amax / 127.0f;
-    // every quotient is computed (by 1 when amax is 0, where the select gives 0 anyway), so
-    // the four divisions are straight-line code the scheduler can interleave
-    const float dq = amax == 0.0f ? 1.0f : d;
+    const bool dok = q8_scale_ok(d);
+    const float inv = 1.0f / (dok ? d : 1.0f);
+    int q[4];
+    u32 slow = 0u;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        bool sl;
+        q[k] = q8_code_fast(v[k], inv, dok, sl);
+        slow |= (sl ? 1u : 0u) << k;
+    }
+    if (__builtin_amdgcn_ballot_w64(slow != 0u) != 0) {      // rare: see q8_code_fast
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (slow & (1u << k)) q[k] = q8_code_exact(v[k], d);
+    }
     u32 packed = 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const int q = (int) roundf(v[k] / dq);
-        const int code = amax == 0.0f ? 0 : q;
+        const int code = amax == 0.0f ? 0 : q[k];
         packed |= ((u32) code & 0xFFu) << (8 * k);
     }
     const int i = j * RMS_CHUNK + 4 * lane;               // first value of this lane in the row
@@ -986,11 +1037,31 @@ __device__ __forceinline__ void quantize_chunks(const v4f xv[N], const v4f nwv[N
     for (int i = 0; i < N; ++i) amax[i] = fmaxf(amax[i], dpp_f<DPP_QUAD_XOR2>(0.0f, amax[i]));
 #pragma unroll
     for (int i = 0; i < N; ++i) amax[i] = fmaxf(amax[i], dpp_f<DPP_ROW_HALF_MIRROR>(0.0f, amax[i]));
-    float d[N], dq[N];
+    float d[N], inv[N];
+    bool dok[N];
 #pragma unroll
     for (int i = 0; i < N; ++i) {
         d[i] = amax[i] / 127.0f;
-        dq[i] = amax[i] == 0.0f ? 1.0f : d[i];
+        dok[i] = q8_scale_ok(d[i]);
+        inv[i] = 1.0f / (dok[i] ? d[i] : 1.0f);
+    }
+    int q[N][4];
+    u32 slow = 0u;
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            bool sl;
+            q[i][k] = q8_code_fast(v[i][k], inv[i], dok[i], sl);
+            slow |= (sl ? 1u : 0u) << (4 * i + k);
+        }
+    // rare (values next to a rounding boundary, degenerate blocks): one wave-uniform branch
+    if (__builtin_amdgcn_ballot_w64(slow != 0u) != 0) {
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (slow & (1u << (4 * i + k))) q[i][k] = q8_code_exact(v[i][k], d[i]);
     }
     u32 packed[N];
 #pragma unroll
@@ -998,8 +1069,7 @@ __device__ __forceinline__ void quantize_chunks(const v4f xv[N], const v4f nwv[N
         packed[i] = 0u;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const int q = (int) roundf(v[i][k] / dq[i]);
-            const int code = amax[i] == 0.0f ? 0 : q;
+            const int code = amax[i] == 0.0f ? 0 : q[i][k];
             packed[i] |= ((u32) code & 0xFFu) << (8 * k);
         }
     }

@@ -123,10 +123,21 @@ __device__ __forceinline__ void gu_prologue(const GemvArgs &a, int t, int p, flo
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");      // the sums are in LDS before the count
     if (lane == 0) __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     wait_lds_count(a, sync, (u32) NP);            // on timeout the row is wrong and the status word says so
-    float ss = 0.0f;                                          // ascending, as every other producer of y
+    // ascending, as every other producer of y: all NP * PC slots are read at once (128-bit
+    // LDS reads, no read waits on an add) and the slots past the row add +0.0, which leaves
+    // the non-negative sum's bits unchanged
+    float rv[NP * PC];
 #pragma unroll
-    for (int j = 0; j < NP * PC; ++j)
-        if (j < nchunk) ss += red[j];
+    for (int j = 0; j < NP * PC; j += 4) {
+        const v4f r4 = *(const v4f *) (red + j);
+        rv[j] = r4.x;
+        rv[j + 1] = r4.y;
+        rv[j + 2] = r4.z;
+        rv[j + 3] = r4.w;
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NP * PC; ++j) ss += j < nchunk ? rv[j] : 0.0f;
     const float scale = 1.0f / sqrtf(ss / (float) K + a.eps);
     int jc[PC];
 #pragma unroll
@@ -214,11 +225,16 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
         return;
     }
     const int sw = wave - NP;
-    const int local0 = (b % a.wg_per_tok) * a.nwaves;         // the workgroup's first step within token t
+    // the first nsh_wg workgroups of a token take sh_per_wg shared steps each, the others
+    // nwaves routed steps each (whole 32-row blocks of one matrix when hq is written)
+    const int bt = b % a.wg_per_tok;
+    const int nsh_wg = a.sh_per_wg > 0 ? (a.sh_tiles_per_tok + a.sh_per_wg - 1) / a.sh_per_wg : 0;
+    const bool sh_wg = bt < nsh_wg;
+    const int local0 = sh_wg ? bt * a.sh_per_wg : a.sh_tiles_per_tok + (bt - nsh_wg) * a.nwaves;
     const int local = local0 + sw;                              // this wave's step
     uint8_t *span = lds + (u32) sw * a.lds_wave;
-    const bool sh = local < a.sh_tiles_per_tok;
-    bool run = local < a.tiles_per_tok && (TS != 0 || !sh);
+    const bool sh = sh_wg;
+    bool run = (sh_wg ? sw < a.sh_per_wg && local < a.sh_tiles_per_tok : local < a.tiles_per_tok) && (TS != 0 || !sh);
     StepCtx s;
     if (run) {
         s = sh ? step_locate(a, true, t * a.sh_tiles_per_tok + local)
@@ -250,7 +266,7 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
             rl = step_store<TW>(a, s, su, sg, v);
         }
     }
-    if (a.hq) gu_block_q8_1(a, t, local0, sw, sh ? a.sh_rps : a.rps, run, rl, v, red + 32, sync + 3);
+    if (a.hq && (!sh_wg || a.hq_sh)) gu_block_q8_1(a, t, local0, sw, sh ? a.sh_rps : a.rps, run, rl, v, red + 32, sync + 3);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");      // a step skipped after a timeout: its DMA has landed
 }
 
@@ -291,7 +307,9 @@ __global__ __launch_bounds__(FFN_DN_MAX_WAVES *WAVE) void mc_ffn_down_combine_ke
         ybytes = (u32) a.sh_y_bytes;
         yrow = (u32) ((int64_t) s.t * a.sh_stride_col_y);
     }
-    const u32 alead = dma_bytes(ybase, ybytes, yrow, a.act_row_bytes, span + a.lds_act);
+    // the shared expert's row may be fp32 (sh_act_f32) beside q8_1 routed rows
+    const bool qf32 = ACT == ACT_F32 || (sh && a.sh_act_f32);
+    const u32 alead = dma_bytes(ybase, ybytes, yrow, sh ? a.sh_act_row_bytes : a.act_row_bytes, span + a.lds_act);
     if (sh) {
         if constexpr (TS != 0) step_issue<TS>(a, s, span);
     } else {
@@ -303,7 +321,7 @@ __global__ __launch_bounds__(FFN_DN_MAX_WAVES *WAVE) void mc_ffn_down_combine_ke
         // the activation row went out first: it is in LDS while the weights still land
         wait_loads_at_most(s.n_up);
         const uint8_t *arow = span + a.lds_act + alead;
-        if constexpr (ACT == ACT_F32) {
+        if (qf32) {
             quantize_row_lds((const float *) arow, span + a.lds_q8, a.ncols);
             arow = span + a.lds_q8;
         }
@@ -445,7 +463,17 @@ static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act) {
         }
         a.rps = rps;
         a.sh_rps = sh_rps;
-        a.wg_per_tok = (a.tiles_per_tok + a.nwaves - 1) / a.nwaves;
+        // shared-expert workgroups of about the bytes of a routed one: the shared matrix rows are
+        // often wider (a larger type), and the launch ends with its slowest workgroup.  Its q8_1
+        // blocks (hq_sh) need whole 32-row workgroups.
+        a.sh_per_wg = 0;
+        if (ts) {
+            const double rstep = (double) rps * rb, sstep = (double) sh_rps * rbs;
+            int n = (a.hq && a.hq_sh) ? a.nwaves : (int) (a.nwaves * rstep / sstep);   // at most a routed one's bytes
+            a.sh_per_wg = n < 1 ? 1 : (n > a.nwaves ? a.nwaves : n);
+        }
+        const int nsh_wg = a.sh_per_wg ? (a.sh_tiles_per_tok + a.sh_per_wg - 1) / a.sh_per_wg : 0;
+        a.wg_per_tok = nsh_wg + (a.tiles_per_tok - a.sh_tiles_per_tok + a.nwaves - 1) / a.nwaves;
         a.lds_y = (uint32_t) a.nwaves * a.lds_wave;
         a.lds_part = a.lds_y + round16((uint32_t) (a.ncols / 32 * 36));
         a.lds_total = a.lds_part + 16u + 4u * 32u + 4u * 32u + 2u * (uint32_t) (a.ncols / 16);
@@ -460,13 +488,14 @@ static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act) {
     // enough workgroups for every CU: at most nrows * n_tok / 256 rows each
     const int fill = (a.nrows * a.n_tok + 255) / 256;
     if (fill < rps) rps = fill < 1 ? 1 : fill;
-    const uint32_t q8_bytes = act == ACT_F32 ? round16((uint32_t) (a.ncols / 32 * 36)) : 0u;
+    const uint32_t q8_bytes = act == ACT_F32 || (ts && a.sh_act_f32) ? round16((uint32_t) (a.ncols / 32 * 36)) : 0u;
+    const uint32_t arow_max = ts && a.sh_act_row_bytes > a.act_row_bytes ? a.sh_act_row_bytes : a.act_row_bytes;
     for (;;) {
         const uint32_t sr = span_bytes((uint32_t) rps, rb);
         const uint32_t ss = ts ? span_bytes((uint32_t) rps, rbs) : 0u;
         a.lds_span = sr > ss ? sr : ss;
         a.lds_act = a.lds_span;
-        a.lds_q8 = a.lds_act + round_up_1k(a.act_row_bytes + 20u);
+        a.lds_q8 = a.lds_act + round_up_1k(arow_max + 20u);
         a.lds_sums = a.lds_q8 + q8_bytes;
         a.lds_wave = a.lds_sums + round16(2u * (uint32_t) (a.ncols / 16));
         a.lds_part = (uint32_t) a.nwaves * a.lds_wave;
@@ -491,6 +520,7 @@ int launch_ffn(GemvArgs a, int tw, int ts, int act, void *stream) {
     if (ts == 0 || !a.sh_up) ts = 0;
     if (a.mode == FFN_GATE_UP_NORM) act = ACT_Q8_1;
     a.act_row_bytes = act == ACT_Q8_1 ? (uint32_t) (a.ncols / 32 * 36) : (uint32_t) a.ncols * 4u;
+    a.sh_act_row_bytes = act == ACT_Q8_1 && !a.sh_act_f32 ? (uint32_t) (a.ncols / 32 * 36) : (uint32_t) a.ncols * 4u;
     hipError_t err = ffn_layout(a, tw, ts, act);
     if (err != hipSuccess) return (int) err;
     if (a.n_tiles <= 0) return (int) hipSuccess;

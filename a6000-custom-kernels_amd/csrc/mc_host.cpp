@@ -498,6 +498,7 @@ struct FfnExtra {
     const float *residual = nullptr;
     float *x_out = nullptr;
     int64_t x_stride = 0;
+    bool sh_act_f32 = false;         // FFN_DOWN_COMBINE: the shared expert's rows are fp32
 };
 
 // Shared validation + launch of the GEMV (and of the fused decode kernels when fx is given).
@@ -588,9 +589,15 @@ int gemv_common(int use_cache, int act, const ggml_hip_moe_tensor *src0, const g
             a.sh_stride_col_dst = fusion->shared_stride_col_dst;
             a.sh_matrix_bytes = (uint64_t) (ne00 / type_geom(ts).block_elems) * type_geom(ts).block_bytes * (uint64_t) ne01;
             if (fusion->shared_src1) {
+                // fp32 shared rows beside q8_1 routed rows: strides in floats
+                const bool shf = fx && fx->sh_act_f32;
+                const int64_t sh_blk = shf ? 4 : ablk_bytes, sh_row = shf ? ne00 * 4 : act_row;
+                if (shf && (((uintptr_t) fusion->shared_src1) & 15u))
+                    return fail(E_INVALID, "moe-ffn: fp32 shared rows must be 16-byte aligned");
+                a.sh_act_f32 = shf ? 1 : 0;
                 a.sh_y = (const uint8_t *) fusion->shared_src1;
-                a.sh_stride_col_y = fusion->shared_stride_col_y * ablk_bytes;
-                a.sh_y_bytes = (uint64_t) ((ncols_dst - 1) * a.sh_stride_col_y + act_row);
+                a.sh_stride_col_y = fusion->shared_stride_col_y * sh_blk;
+                a.sh_y_bytes = (uint64_t) ((ncols_dst - 1) * a.sh_stride_col_y + sh_row);
             }
         }
     }
@@ -935,8 +942,6 @@ int ggml_hip_moe_ffn_gate_up_norm(int use_cache, const ggml_hip_moe_tensor *src0
         if (ne00 / 256 > 16) return fail(E_UNSUPPORTED, "moe-ffn: q8_1 outputs need at most 16 units per row");
         if ((((uintptr_t) dst_q8_1) | ((uintptr_t) shared_dst_q8_1)) & 3u)
             return fail(E_INVALID, "moe-ffn: q8_1 outputs must be 4-byte aligned");
-        if (fusion && fusion->shared_up && !shared_dst_q8_1)
-            return fail(E_INVALID, "moe-ffn: q8_1 outputs with a shared expert need shared_dst_q8_1");
     }
     if (use_cache && !wants_impl(src0)) return fail(E_STATE, "moe-cache: src0 does not qualify for the cache path (wants() == 0)");
     if (!use_cache && gate_host) return fail(E_INVALID, "moe-gemv: gate_host is for the cache path; pass fusion->gate");
@@ -972,6 +977,8 @@ int ggml_hip_moe_ffn_down_combine(int use_cache, int act_format, const ggml_hip_
                                   int64_t stride_channel_y, int64_t stride_col_x, int64_t ids_stride, void *stream) {
     if (!router_w || !x_out) return fail(E_INVALID, "moe-ffn: null router weights or x_out");
     if (use_cache && !wants_impl(src0)) return fail(E_STATE, "moe-cache: src0 does not qualify for the cache path (wants() == 0)");
+    const bool sh_f32 = (act_format & GGML_HIP_MOE_ACT_SHARED_F32) != 0;
+    act_format &= ~GGML_HIP_MOE_ACT_SHARED_F32;
     if (act_format != ACT_Q8_1 && act_format != ACT_F32) return fail(E_UNSUPPORTED, "moe-ffn: down activations are q8_1 or fp32 rows");
     if (fusion && (fusion->gate || fusion->shared_gate || fusion->gate_bias || fusion->gate_scale))
         return fail(E_INVALID, "moe-ffn: the down projection takes no gate");
@@ -980,6 +987,7 @@ int ggml_hip_moe_ffn_down_combine(int use_cache, int act_format, const ggml_hip_
     if ((((uintptr_t) x_out) | ((uintptr_t) residual) | ((uintptr_t) router_w)) & 3u) return fail(E_INVALID, "moe-ffn: misaligned fp32 buffers");
     FfnExtra fx;
     fx.mode = FFN_DOWN_COMBINE;
+    fx.sh_act_f32 = sh_f32 || act_format == ACT_F32;
     fx.router_w = router_w;
     fx.residual = residual;
     fx.x_out = x_out;

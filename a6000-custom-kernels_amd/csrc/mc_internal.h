@@ -109,6 +109,8 @@ struct GemvArgs {
     const uint8_t *sh_y;          // null: channel 0 of y
     uint64_t sh_y_bytes;
     int64_t sh_stride_col_y;      // bytes between tokens of sh_y
+    int32_t sh_act_f32;           // FFN_DOWN_COMBINE: sh_y rows are fp32 (quantized by the shared wave)
+    uint32_t sh_act_row_bytes;    // bytes of one sh_y row
     uint64_t sh_matrix_bytes;     // bytes of the shared matrix
     // shape
     int32_t ncols;                // K (ne00)
@@ -131,6 +133,9 @@ struct GemvArgs {
     // fused decode kernels (mc_ffn.hip); FFN_NONE: the plain MUL_MAT_ID GEMV
     int32_t mode;
     int32_t nwaves;               // step waves per workgroup (FFN_GATE_UP_NORM: plus FFN_GU_PRO_WAVES)
+    int32_t sh_per_wg;            // FFN_GATE_UP_NORM: steps of a shared-expert workgroup (its first
+                                  //   workgroups take only shared steps, about as many bytes as the
+                                  //   routed workgroups' nwaves steps)
     int32_t wg_per_tok;           // workgroups per token
     int32_t tiles_per_tok;        // steps per token: shared tiles first, then the routed picks'
     uint32_t lds_wave;            // LDS bytes of one wave's region (spans, activation staging)

@@ -34,7 +34,7 @@ import math
 
 import numpy as np
 
-from . import (ACT_F32, ACT_Q8_1, BLOCK, GLU_SWIGLU, KQUANTS, Q2_K, Q3_K, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0, check,
+from . import (ACT_F32, ACT_Q8_1, ACT_SHARED_F32, BLOCK, GLU_SWIGLU, KQUANTS, Q2_K, Q3_K, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0, check,
                lib, make_fusion, make_tensor, row_bytes)
 
 # byte offsets of the fp16 block-scale fields per type, and the value written there
@@ -69,9 +69,13 @@ class Layer:
 
 class MoeDecodeModel:
     def __init__(self, torch, n_layers=48, n_experts=512, hidden=4096, ffn=768, n_used=8, wtype=Q2_K,
-                 sh_type=Q4_K, seed=0, device="cuda", residual=True, fused=True):
+                 sh_type=Q4_K, seed=0, device="cuda", residual=True, fused=True, shared_q8=True):
         self.torch = torch
         self.fused = fused
+        # fused plan: the gate/up launch writes the shared expert's q8_1 row (32-row shared
+        # workgroups) or only its fp32 row, which the down launch quantizes (shared
+        # workgroups of a routed one's bytes)
+        self.shared_q8 = shared_q8
         self.L, self.E, self.H, self.F, self.U = n_layers, n_experts, hidden, ffn, n_used
         self.wtype, self.sh_type = wtype, sh_type
         self.residual = residual
@@ -118,15 +122,15 @@ class MoeDecodeModel:
     def gate_up_bytes(self):
         H, F, U = self.H, self.F, self.U
         w = U * 2 * row_bytes(self.wtype, H) * F + 2 * row_bytes(self.sh_type, H) * F
-        if self.fused:                                 # x row + norm weight in, GLU rows (fp32 + q8_1) out
-            return w + 2 * H * 4 + (U + 1) * F * 4 + (U + 1) * F // 32 * 36
+        if self.fused:                                 # x row + norm weight in, GLU rows (fp32 + routed q8_1) out
+            return w + 2 * H * 4 + (U + 1) * F * 4 + U * F // 32 * 36
         return w + H // 32 * 36 + (U + 1) * F * 4      # q8_1 row in, GLU rows out
 
     def down_bytes(self):
         H, F, U = self.H, self.F, self.U
         w = U * row_bytes(self.wtype, F) * H + row_bytes(self.sh_type, F) * H
-        if self.fused:                                 # q8_1 GLU rows, residual, router weights in; x out
-            return w + (U + 1) * F // 32 * 36 + 2 * H * 4 + U * 4
+        if self.fused:                                 # routed q8_1 + shared fp32 GLU rows, residual, router weights in; x out
+            return w + U * F // 32 * 36 + F * 4 + 2 * H * 4 + U * 4
         return w + (U + 1) * F * 4 + (U + 1) * H * 4   # GLU rows in, expert outputs out
 
     def combine_bytes(self):
@@ -178,7 +182,8 @@ class MoeDecodeModel:
                                                   self.norm[l].data_ptr(), self.eps, self.ids[l].data_ptr(),
                                                   self.h.data_ptr(), H, F, self.E, 1, U, H, U * F, F, U, None, 0,
                                                   self.hq.data_ptr(), (U + 1) * nb, nb,
-                                                  self.hq[U:].data_ptr(), (U + 1) * nb, s),
+                                                  self.hq[U:].data_ptr() if self.shared_q8 else None,
+                                                  (U + 1) * nb, s),
               "gate_up_norm")
 
     def launch_down_combine(self, l, src, dst, s=None):
@@ -187,7 +192,9 @@ class MoeDecodeModel:
         s = s or self._stream()
         H, F, U = self.H, self.F, self.U
         nb = F // 32
-        check(lib().ggml_hip_moe_ffn_down_combine(0, ACT_Q8_1, C.byref(ly.t_down), C.byref(ly.f_dnq),
+        act = ACT_Q8_1 if self.shared_q8 else ACT_Q8_1 | ACT_SHARED_F32
+        check(lib().ggml_hip_moe_ffn_down_combine(0, act, C.byref(ly.t_down),
+                                                  C.byref(ly.f_dnq if self.shared_q8 else ly.f_dn),
                                                   self.hq.data_ptr(), self.ids[l].data_ptr(), self.w[l].data_ptr(),
                                                   src.data_ptr() if self.residual else None, dst.data_ptr(),
                                                   F, H, self.E, 1, U, (U + 1) * nb, nb, H, U, s),

@@ -450,6 +450,9 @@ def main():
     ap.add_argument("--kernel-rounds", type=int, default=10)
     ap.add_argument("--plan", choices=("fused", "ops"), default="fused",
                     help="fused: 2 launches per layer (default); ops: gate/up, down, combine launches")
+    ap.add_argument("--shared-rows", choices=("q8_1", "f32"), default="q8_1",
+                    help="fused plan: the gate/up launch writes the shared expert's q8_1 row (q8_1), or only its "
+                         "fp32 row, quantized by the down launch, with byte-balanced shared workgroups (f32)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: a 1 GiB copy (the counter calibration) and the gate/up "
                          "GEMV of every layer, then exit")
@@ -483,7 +486,7 @@ def main():
         return
     t0 = time.perf_counter()
     fused = args.plan == "fused"
-    model = md.MoeDecodeModel(torch, n_layers=args.layers, fused=fused)
+    model = md.MoeDecodeModel(torch, n_layers=args.layers, fused=fused, shared_q8=args.shared_rows == "q8_1")
     torch.cuda.synchronize()
     log(f"weights ready: {args.layers} layers in {time.perf_counter() - t0:.1f}s, "
         f"{torch.cuda.memory_allocated() / 2**30:.1f} GiB allocated")
@@ -557,7 +560,8 @@ def main():
                                "top-8, Q2_K routed gate/up/down + Q4_K shared expert, fused SwiGLU, all resident",
                    "layers": model.L, "experts": model.E, "hidden": model.H, "ffn": model.F, "top_k": model.U,
                    "routed_type": "q2_K", "shared_type": "q4_K", "batch": 1,
-                   "plan": f"{args.plan}: {2 if fused else 3} launches per layer"},
+                   "plan": f"{args.plan}: {2 if fused else 3} launches per layer",
+                   "shared_rows": args.shared_rows},
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "tok_per_s": round(tok_s, 2),
         "bytes_per_step": bpt,

@@ -76,8 +76,10 @@ enum {
 enum {
     GGML_HIP_MOE_ACT_Q8_1 = 0, /* ggml-CUDA q8_1 blocks (36 B / 32 values): the reference's src1_q8_1 */
     GGML_HIP_MOE_ACT_Q8_K = 1, /* ggml-CPU q8_K blocks (292 B / 256 values), K-quant weights only */
-    GGML_HIP_MOE_ACT_F32  = 2  /* fp32 rows, quantized to q8_1 inside the GEMV with the codes and
+    GGML_HIP_MOE_ACT_F32  = 2, /* fp32 rows, quantized to q8_1 inside the GEMV with the codes and
                                   scales ggml_hip_quantize_q8_1 produces (fuses that launch away) */
+    GGML_HIP_MOE_ACT_SHARED_F32 = 0x100  /* ggml_hip_moe_ffn_down_combine flag: the shared
+                                            expert's rows are fp32 (quantized in the launch) */
 };
 
 /* POD mirror of the ggml_tensor fields the path reads
@@ -243,11 +245,14 @@ int ggml_hip_moe_combine_q8_1(const float *o, int64_t o_stride, const float *w, 
  * Every pick and the shared expert (fusion->shared_src1 must be NULL) read y[t].
  * x: [ncols_dst][stride_col_x] floats, 16-byte aligned rows; ne00 % 256 == 0, ne00 <= 8192.
  * y_out (optional): receives y, rows y_out_stride q8_1 blocks apart.
- * dst_q8_1 / shared_dst_q8_1 (optional, both or neither with a shared expert): the q8_1
- * quantization of the outputs (the down projection's input, as ggml_hip_quantize_q8_1 of
- * dst would give), pick c of token t at dst_q8_1 + (t*q8_stride_col + c*q8_stride_channel)
- * q8_1 blocks, the shared expert's at shared_dst_q8_1 + t*shared_q8_stride_col blocks;
- * needs ne01 % 32 == 0 and at most 16 units per row (ne00 <= 4096). */
+ * dst_q8_1 / shared_dst_q8_1 (optional): the q8_1 quantization of the outputs (the down
+ * projection's input, as ggml_hip_quantize_q8_1 of dst would give), pick c of token t at
+ * dst_q8_1 + (t*q8_stride_col + c*q8_stride_channel) q8_1 blocks, the shared expert's at
+ * shared_dst_q8_1 + t*shared_q8_stride_col blocks; needs ne01 % 32 == 0 and at most 16 units
+ * per row (ne00 <= 4096).  With dst_q8_1 but no shared_dst_q8_1 the shared expert's rows are
+ * only written in fp32 (fusion->shared_dst); the launch then splits the shared matrix into
+ * workgroups of about a routed workgroup's bytes, and the down projection quantizes that
+ * row itself (GGML_HIP_MOE_ACT_SHARED_F32). */
 int ggml_hip_moe_ffn_gate_up_norm(
         int use_cache, const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *gate_host,
         const ggml_hip_moe_fusion *fusion, const float *x, const float *norm_weight, float eps,
@@ -264,7 +269,11 @@ int ggml_hip_moe_ffn_gate_up_norm(
  *   x_out[t] = residual[t] + shared[t] + sum_{c < n_used} router_w[t][c] * o_c[t]   (c ascending, fused multiply-add)
  * residual may be NULL or equal to x_out; router_w: [ncols_dst][n_used]; x rows
  * stride_col_x floats apart; n_used (+1 with a shared expert) <= 12.  x_bias / x_scale
- * fusion apply to the routed picks; an out-of-range expert id contributes 0. */
+ * fusion apply to the routed picks; an out-of-range expert id contributes 0.
+ * act_format | GGML_HIP_MOE_ACT_SHARED_F32: fusion->shared_src1 holds fp32 rows
+ * (fusion->shared_stride_col_y floats apart, 16-byte aligned) beside q8_1 routed rows; the
+ * shared wave quantizes its row with the q8_1 quantizer's arithmetic (same results as
+ * passing that row's ggml_hip_quantize_q8_1). */
 int ggml_hip_moe_ffn_down_combine(
         int use_cache, int act_format, const ggml_hip_moe_tensor *src0, const ggml_hip_moe_fusion *fusion,
         const void *src1, const int32_t *ids_d, const float *router_w, const float *residual, float *x_out,

@@ -34,21 +34,25 @@ def _norm_q8_1(torch, mc, x, nw, eps):
     return y
 
 
-@pytest.mark.parametrize("wtype,sh_type,K,R,n_tok,with_nw,bad_id", [
-    ("Q2_K", "Q4_K", 1024, 256, 1, True, False),
-    ("Q2_K", "Q4_K", 4096, 96, 3, True, True),
-    ("Q4_K", "Q6_K", 2048, 160, 2, False, False),
-    ("Q3_K", None, 1024, 128, 1, True, False),
-    ("Q6_K", "Q5_K", 1024, 64, 2, True, True),
-    ("Q5_K", "Q2_K", 768, 200, 1, True, False),
+@pytest.mark.parametrize("wtype,sh_type,K,R,n_tok,with_nw,bad_id,sh_q8", [
+    ("Q2_K", "Q4_K", 1024, 256, 1, True, False, True),
+    ("Q2_K", "Q4_K", 4096, 96, 3, True, True, True),
+    ("Q4_K", "Q6_K", 2048, 160, 2, False, False, True),
+    ("Q3_K", None, 1024, 128, 1, True, False, True),
+    ("Q6_K", "Q5_K", 1024, 64, 2, True, True, True),
+    ("Q5_K", "Q2_K", 768, 200, 1, True, False, True),
     # rows longer than 16 chunks: eight chunks per prologue wave
-    ("Q2_K", "Q4_K", 6144, 96, 2, True, True),
-    ("Q4_K", "Q2_K", 8192, 64, 1, False, False),
+    ("Q2_K", "Q4_K", 6144, 96, 2, True, True, True),
+    ("Q4_K", "Q2_K", 8192, 64, 1, False, False, True),
+    # routed q8_1 copies without the shared one: shared-expert workgroups sized by bytes
+    ("Q2_K", "Q4_K", 4096, 768, 1, True, False, False),
+    ("Q2_K", "Q6_K", 2048, 96, 3, True, True, False),
+    ("Q4_K", "Q2_K", 1024, 256, 2, False, False, False),
 ])
-def test_gate_up_norm_equals_norm_then_gemv(torch_gpu, mc, wtype, sh_type, K, R, n_tok, with_nw, bad_id):
+def test_gate_up_norm_equals_norm_then_gemv(torch_gpu, mc, wtype, sh_type, K, R, n_tok, with_nw, bad_id, sh_q8):
     torch = torch_gpu
     md = import_module("a6000_custom_kernels_amd.moe_decode")
-    _note(f"gate_up_norm {wtype}/{sh_type} K={K} R={R} tok={n_tok} nw={with_nw} bad_id={bad_id}")
+    _note(f"gate_up_norm {wtype}/{sh_type} K={K} R={R} tok={n_tok} nw={with_nw} bad_id={bad_id} sh_q8={sh_q8}")
     E, U, eps = 16, 4, 1e-6
     tw = getattr(mc, wtype)
     ts = getattr(mc, sh_type) if sh_type else None
@@ -83,7 +87,7 @@ def test_gate_up_norm_equals_norm_then_gemv(torch_gpu, mc, wtype, sh_type, K, R,
                        shared_dst=sh if ts else None, shared_type=ts if ts else -1)
     q8 = R % 32 == 0 and K <= 4096            # q8_1 copies of the outputs need 32-row blocks
     dq = torch.zeros((n_tok, U, R // 32 * 36), dtype=torch.uint8, device="cuda") if q8 else None
-    shq = torch.zeros((n_tok, R // 32 * 36), dtype=torch.uint8, device="cuda") if q8 and ts else None
+    shq = torch.zeros((n_tok, R // 32 * 36), dtype=torch.uint8, device="cuda") if q8 and ts and sh_q8 else None
     mc.ffn_gate_up_norm(wtype=tw, weights=up, ids=ids, x=x, dst=dst, K=K, R=R, n_experts=E, norm_weight=nw, eps=eps,
                         fusion=f, y_out=y_out, dst_q8_1=dq, shared_dst_q8_1=shq)
     torch.cuda.synchronize()
@@ -97,7 +101,7 @@ def test_gate_up_norm_equals_norm_then_gemv(torch_gpu, mc, wtype, sh_type, K, R,
             for c in range(U):
                 if ids_np[ti, c] >= 0:
                     assert torch.equal(dq[ti, c], mc.quantize_q8_1(dst[ti, c].view(1, R))[0]), (ti, c)
-            if ts:
+            if ts and sh_q8:
                 assert torch.equal(shq[ti], mc.quantize_q8_1(sh[ti].view(1, R))[0])
     if bad_id:
         assert bool((dst[-1, 1] == SENTINEL).all())
@@ -107,6 +111,9 @@ def test_gate_up_norm_equals_norm_then_gemv(torch_gpu, mc, wtype, sh_type, K, R,
 @pytest.mark.parametrize("wtype,sh_type,K,R,n_tok,U,act,residual,fuse_bias,bad_id", [
     ("Q2_K", "Q4_K", 768, 4096, 1, 8, "f32", True, False, False),
     ("Q2_K", "Q4_K", 512, 1024, 2, 4, "q8_1", True, False, True),
+    # q8_1 routed rows, fp32 shared rows quantized by the shared wave
+    ("Q2_K", "Q4_K", 768, 4096, 1, 8, "q8_1+shf32", True, False, False),
+    ("Q3_K", "Q6_K", 512, 512, 3, 4, "q8_1+shf32", True, True, True),
     ("Q5_K", None, 768, 1280, 3, 6, "f32", False, True, False),      # 15-row tiles, the last one partial
     ("Q3_K", "Q6_K", 512, 512, 3, 4, "f32", True, True, True),
     ("Q6_K", "Q4_K", 1024, 512, 1, 11, "q8_1", True, False, False),   # 12 waves per workgroup
@@ -122,6 +129,7 @@ def test_down_combine_equals_gemv_then_combine(torch_gpu, mc, wtype, sh_type, K,
     tw = getattr(mc, wtype)
     ts = getattr(mc, sh_type) if sh_type else None
     act_fmt = mc.ACT_F32 if act == "f32" else mc.ACT_Q8_1
+    sh_f32 = act == "q8_1+shf32"
     gen = torch.Generator(device="cuda")
     gen.manual_seed(K + R + U)
     down = md.random_expert_tensor(torch, tw, E, R, K, gen)
@@ -157,9 +165,10 @@ def test_down_combine_equals_gemv_then_combine(torch_gpu, mc, wtype, sh_type, K,
 
     x_out = torch.full((n_tok, R), SENTINEL, dtype=torch.float32, device="cuda")
     f = mc.make_fusion(x_bias=bias, x_scale=scale, shared_up=sh_down, shared_type=ts if ts else -1,
-                       shared_src1=hs if ts else None, shared_stride_col_y=sh_stride, bias_stride=R)
+                       shared_src1=(hs_f if sh_f32 else hs) if ts else None,
+                       shared_stride_col_y=K if sh_f32 else sh_stride, bias_stride=R)
     mc.ffn_down_combine(wtype=tw, weights=down, ids=ids, h=h, router_w=w, x_out=x_out, K=K, R=R, n_experts=E,
-                        residual=x, act=act_fmt, fusion=f)
+                        residual=x, act=act_fmt | (mc.ACT_SHARED_F32 if sh_f32 else 0), fusion=f)
     torch.cuda.synchronize()
     assert bool(torch.isfinite(x_ref).all())
     assert torch.equal(x_out, x_ref)
