@@ -30,6 +30,7 @@ GLU_REGLU, GLU_GEGLU, GLU_SWIGLU, GLU_SWIGLU_OAI, GLU_GEGLU_ERF, GLU_GEGLU_QUICK
 # activation formats
 ACT_Q8_1, ACT_Q8_K, ACT_F32 = 0, 1, 2
 ACT_SHARED_F32 = 0x100       # ffn_down_combine flag: the shared expert's rows are fp32
+ACT_DOT_Q8_K = 0x200         # ffn_down_combine flag (fp32 rows): the dots run on q8_K of the rows
 # graph node ops for fusion detection
 OP_MUL_MAT, OP_MUL_MAT_ID, OP_ADD_ID, OP_MUL, OP_ADD, OP_GLU, OP_OTHER = range(1, 8)
 
@@ -102,6 +103,9 @@ SIGNATURES = [
      [_VP, _I64, _VP, _I32, _VP, _I64, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP, C.c_float, _VP]),
     ("ggml_hip_moe_ffn_gate_up_norm", C.c_int,
      [C.c_int, C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Fusion), _VP, _VP, C.c_float, _VP, _VP]
+     + [_I64] * 3 + [_I64] * 2 + [_I64] * 4 + [_VP, _I64, _VP, _I64, _I64, _VP, _I64, _VP]),
+    ("ggml_hip_moe_ffn_gate_up_norm_ex", C.c_int,
+     [C.c_int, C.c_int, C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Fusion), _VP, _VP, C.c_float, _VP, _VP]
      + [_I64] * 3 + [_I64] * 2 + [_I64] * 4 + [_VP, _I64, _VP, _I64, _I64, _VP, _I64, _VP]),
     ("ggml_hip_moe_ffn_down_combine", C.c_int,
      [C.c_int, C.c_int, C.POINTER(Tensor), C.POINTER(Fusion), _VP, _VP, _VP, _VP, _VP]
@@ -293,10 +297,11 @@ def mul_mat_vec(*, wtype, weights, ids, y, dst, K, R, n_experts, use_cache=False
 
 def ffn_gate_up_norm(*, wtype, weights, ids, x, dst, K, R, n_experts, norm_weight=None, eps=1e-6,
                      fusion: Fusion | None = None, y_out=None, dst_q8_1=None, shared_dst_q8_1=None, use_cache=False,
-                     gate_host=None, name="", stream=None, weights_ptr=None, gate_ptr=None):
-    """Gate/up GEMV whose q8_1 activation is RMSNorm(x) * norm_weight, computed in the same launch
-    (ggml_hip_moe_ffn_gate_up_norm).  x: fp32 [n_tok, K] (device, 16-byte aligned rows);
-    ids: int32 [n_tok, n_used]; dst: float32 [n_tok, n_used, R]; y_out: optional uint8 [n_tok, K/32*36];
+                     gate_host=None, name="", stream=None, weights_ptr=None, gate_ptr=None, act=ACT_Q8_1):
+    """Gate/up GEMV whose activation is RMSNorm(x) * norm_weight, quantized to q8_1 (act=ACT_Q8_1) or
+    q8_K (act=ACT_Q8_K) in the same launch (ggml_hip_moe_ffn_gate_up_norm_ex).  x: fp32 [n_tok, K]
+    (device, 16-byte aligned rows); ids: int32 [n_tok, n_used]; dst: float32 [n_tok, n_used, R];
+    y_out: optional uint8 [n_tok, K/32*36] (q8_1) or [n_tok, K/256*292] (q8_K);
     dst_q8_1 / shared_dst_q8_1: optional uint8 [n_tok, n_used, R/32*36] / [n_tok, R/32*36] q8_1 copies."""
     n_tok, n_used = ids.shape
     _require_gpu(ids, x, dst, norm_weight, y_out)
@@ -304,11 +309,12 @@ def ffn_gate_up_norm(*, wtype, weights, ids, x, dst, K, R, n_experts, norm_weigh
     ptr = weights_ptr if weights_ptr is not None else weights.data_ptr()
     src0 = make_tensor(wtype, K, R, n_experts, ptr, name=name, keep=keep)
     g = make_tensor(wtype, K, R, n_experts, gate_ptr, name=name.replace("up", "gate"), keep=keep) if gate_ptr else None
-    rc = lib().ggml_hip_moe_ffn_gate_up_norm(
-        1 if use_cache else 0, C.byref(src0), C.byref(g) if g is not None else None,
+    yblk = 292 if act == ACT_Q8_K else 36
+    rc = lib().ggml_hip_moe_ffn_gate_up_norm_ex(
+        1 if use_cache else 0, act, C.byref(src0), C.byref(g) if g is not None else None,
         C.byref(fusion) if fusion is not None else None, x.data_ptr(), _ptr(norm_weight), eps, ids.data_ptr(),
         dst.data_ptr(), K, R, n_experts, n_tok, n_used, x.stride(0), n_used * R, R, ids.stride(0),
-        _ptr(y_out), y_out.stride(0) // 36 if y_out is not None else 0,
+        _ptr(y_out), y_out.stride(0) // yblk if y_out is not None else 0,
         _ptr(dst_q8_1), dst_q8_1.stride(0) // 36 if dst_q8_1 is not None else 0,
         dst_q8_1.stride(1) // 36 if dst_q8_1 is not None else 0,
         _ptr(shared_dst_q8_1), shared_dst_q8_1.stride(0) // 36 if shared_dst_q8_1 is not None else 0, _stream(stream))

@@ -107,7 +107,19 @@ template <int UE, int ACT, bool S16 = false>
 __device__ __forceinline__ void load_act_lds(Act<UE> &A, const uint8_t *p, const int16_t *s16 = nullptr) {
     constexpr int NW = ACT == ACT_Q8_1 ? UE / 32 * 9 : 73;
     u32 w[NW];
-    if (NW % 4 == 0 && ((uintptr_t) p & 15u) == 0) {
+    if (NW % 4 == 1 && ((uintptr_t) p & 15u) == 0) {
+        // a 16-byte aligned q8_K block (the padded LDS rows): 18 128-bit reads and one 32-bit read
+        const v4u *q = (const v4u *) __builtin_assume_aligned(p, 16);
+#pragma unroll
+        for (int i = 0; i < NW / 4; ++i) {
+            const v4u v = q[i];
+            w[4 * i] = v.x;
+            w[4 * i + 1] = v.y;
+            w[4 * i + 2] = v.z;
+            w[4 * i + 3] = v.w;
+        }
+        w[NW - 1] = ((const u32 *) p)[NW - 1];
+    } else if (NW % 4 == 0 && ((uintptr_t) p & 15u) == 0) {
         const v4u *q = (const v4u *) __builtin_assume_aligned(p, 16);
 #pragma unroll
         for (int i = 0; i < NW / 4; ++i) {
@@ -138,11 +150,11 @@ __device__ __forceinline__ void load_act_lds(Act<UE> &A, const uint8_t *p, const
         for (int k = 0; k < 64; ++k) A.q[k] = w[1 + k];
     }
     if constexpr (S16) {
-        // the 16-value sums precomputed next to the row (exact integer sums of the same codes)
-        const u32 *sw = (const u32 *) s16;
+        // the 16-value sums precomputed next to the row (exact integer sums of the same codes):
+        // a separate int16 array for q8_1 rows, the block's own bsums for q8_K
 #pragma unroll
         for (int i = 0; i < UE / 32; ++i) {
-            const u32 pair = sw[i];
+            const u32 pair = ACT == ACT_Q8_K ? w[65 + i] : ((const u32 *) s16)[i];
             A.s2[i] = pair;
             A.s16[2 * i] = (int) (int16_t) (pair & 0xFFFFu);
             A.s16[2 * i + 1] = (int) (int16_t) (pair >> 16);
@@ -968,6 +980,127 @@ __device__ __forceinline__ void quantize_chunk(const float xv[4], bool norm, flo
     *(u32 *) (yb + 4 + (i % 32)) = packed;
     // the eight lanes of a block store the same scale word (no branch around the store)
     *(u32 *) yb = (u32) f2h_bits(d) | (WITH_SUM ? ((u32) f2h_bits(sum) << 16) : 0u);
+}
+
+// One 64-lane wave: the q8_K blocks (292 bytes at yb[i]: d, qs[256], bsums[16]) of N groups
+// of 256 values v[i], lane l holding values 4l .. 4l+3 of each, with the arithmetic of
+// ggml's quantize_row_q8_K_ref: max = the signed value of the first largest |v| (strictly
+// larger wins, so the lowest index among ties), iscale = -127 / max,
+// q = min(127, rint(iscale * v)) (round half to even, as its nearest_int), d = 1 / iscale,
+// bsums = sums of each 16 codes; an all-zero block gets d = 0 and zero codes and sums.
+// The N blocks go stage by stage so their dependency chains (cross-lane maxima, divisions)
+// interleave; cross-lane steps stay on DPP / permlane (no LDS traffic).  With `second`,
+// yb2[i] receives a copy of each block.
+template <int N>
+__device__ __forceinline__ void q8K_chunks(const float (&v)[N][4], uint8_t *const (&yb)[N], uint8_t *const (&yb2)[N],
+                                           bool second) {
+    const int lane = threadIdx.x % WAVE;
+    float am[N], amax[N], cand[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        am[i] = -1.0f;
+        cand[i] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float ax = fabsf(v[i][j]);
+            if (ax > am[i]) {
+                am[i] = ax;
+                cand[i] = v[i][j];
+            }
+        }
+        amax[i] = am[i];
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) amax[i] = fmaxf(amax[i], xor_lanes<32>(amax[i]));
+#pragma unroll
+    for (int i = 0; i < N; ++i) amax[i] = fmaxf(amax[i], xor_lanes<16>(amax[i]));
+#pragma unroll
+    for (int i = 0; i < N; ++i) amax[i] = fmaxf(amax[i], xor_lanes<8>(amax[i]));
+#pragma unroll
+    for (int i = 0; i < N; ++i) amax[i] = fmaxf(amax[i], xor_lanes<4>(amax[i]));
+#pragma unroll
+    for (int i = 0; i < N; ++i) amax[i] = fmaxf(amax[i], xor_lanes<2>(amax[i]));
+#pragma unroll
+    for (int i = 0; i < N; ++i) amax[i] = fmaxf(amax[i], xor_lanes<1>(amax[i]));
+    float d[N], iscale[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        // the lowest lane holding the maximum, and its first such value
+        const uint64_t hit = __builtin_amdgcn_ballot_w64(am[i] == amax[i]);
+        const int l0 = hit ? __builtin_ctzll(hit) : 0;
+        const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cand[i]), l0));
+        // (all-NaN lanes leave amax at -1: a zero block)
+        iscale[i] = amax[i] > 0.0f ? -127.0f / mx : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) d[i] = amax[i] > 0.0f ? 1.0f / iscale[i] : 0.0f;
+    u32 packed[N];
+    int sum[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        packed[i] = 0u;
+        sum[i] = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float p;
+            {
+#pragma clang fp contract(off)
+                p = iscale[i] * v[i][j];
+            }
+            int c = (int) __builtin_rintf(p);
+            c = amax[i] > 0.0f ? (c < 127 ? c : 127) : 0;
+            packed[i] |= ((u32) c & 0xFFu) << (8 * j);
+            sum[i] += c;                                 // 16 codes = 4 lanes
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) sum[i] += __builtin_amdgcn_update_dpp(0, sum[i], DPP_QUAD_XOR1, 0xF, 0xF, false);
+#pragma unroll
+    for (int i = 0; i < N; ++i) sum[i] += __builtin_amdgcn_update_dpp(0, sum[i], DPP_QUAD_XOR2, 0xF, 0xF, false);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            if (c == 1 && !second) continue;
+            uint8_t *y = c == 0 ? yb[i] : yb2[i];
+            *(u32 *) (y + 4 + 4 * lane) = packed[i];
+            if ((lane & 3) == 0) *(int16_t *) (y + 260 + 2 * (lane >> 2)) = (int16_t) sum[i];
+            if (lane == 0) *(float *) y = d[i];
+        }
+    }
+}
+
+// Stride of q8_K blocks in the fused kernels' LDS rows: 292 bytes padded to a 16-byte
+// multiple, so every block is read with 128-bit LDS reads.
+constexpr int Q8K_LDS_STRIDE = 304;
+
+__device__ __forceinline__ void quantize_row_lds_q8K(const float *x, uint8_t *q, int k) {
+    constexpr int G = 4;                                   // blocks interleaved per pass
+    const int lane = threadIdx.x % WAVE;
+    const bool al = ((uintptr_t) x & 15u) == 0;
+    const int nblk = k / 256;
+    for (int b0 = 0; b0 < nblk; b0 += G) {
+        float v[G][4];
+        uint8_t *yb[G];
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            const int b = min(b0 + i, nblk - 1);           // past the row: the last block again, same bytes
+            const float *src = x + 256 * b + 4 * lane;
+            if (al) {
+                const v4f x4 = *(const v4f *) __builtin_assume_aligned(src, 16);
+                v[i][0] = x4.x;
+                v[i][1] = x4.y;
+                v[i][2] = x4.z;
+                v[i][3] = x4.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[i][j] = src[j];
+            }
+            yb[i] = q + Q8K_LDS_STRIDE * b;
+        }
+        q8K_chunks<G>(v, yb, yb, false);
+    }
+    wave_lds_sync();
 }
 
 // 16-value sums of the codes of a q8_1 row of k values in LDS (36-byte blocks from p,

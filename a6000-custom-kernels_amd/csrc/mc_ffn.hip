@@ -99,7 +99,7 @@ __device__ __forceinline__ bool wait_lds_count(const GemvArgs &a, const u32 *cnt
 // publishes the chunks' canonical sums and counts them in sync[0], waits for the
 // other prologue waves' sums, and writes q8_1((x * scale) * nw) of its chunks to the
 // LDS row (and to y_out when asked), counted in sync[1].
-template <int PC>
+template <int PC, int AQ>
 __device__ __forceinline__ void gu_prologue(const GemvArgs &a, int t, int p, float *red, uint8_t *ys, int16_t *s16,
                                             u32 *sync, bool write_y_out) {
     constexpr int NP = FFN_GU_PRO_WAVES;
@@ -142,13 +142,29 @@ __device__ __forceinline__ void gu_prologue(const GemvArgs &a, int t, int p, flo
     int jc[PC];
 #pragma unroll
     for (int ci = 0; ci < PC; ++ci) jc[ci] = min(p + NP * ci, nchunk - 1);
-    quantize_chunks<PC>(xv, nwv, scale, ys, jc, s16);
-    if (write_y_out) {
+    if constexpr (AQ == ACT_Q8_K) {
+        // one q8_K block per chunk (256 values), written to the LDS row and to y_out when asked
+        float v[PC][4];
+        uint8_t *yb[PC], *yo[PC];
 #pragma unroll
         for (int ci = 0; ci < PC; ++ci) {
-            const float x4[4] = {xv[ci].x, xv[ci].y, xv[ci].z, xv[ci].w};
-            quantize_chunk<true>(x4, true, scale, nwv[ci], a.y_out + (int64_t) t * a.y_out_stride,
-                                 min(p + NP * ci, nchunk - 1));
+            v[ci][0] = (xv[ci].x * scale) * nwv[ci].x;
+            v[ci][1] = (xv[ci].y * scale) * nwv[ci].y;
+            v[ci][2] = (xv[ci].z * scale) * nwv[ci].z;
+            v[ci][3] = (xv[ci].w * scale) * nwv[ci].w;
+            yb[ci] = ys + Q8K_LDS_STRIDE * jc[ci];
+            yo[ci] = a.y_out + (int64_t) t * a.y_out_stride + 292 * jc[ci];     // used only with write_y_out
+        }
+        q8K_chunks<PC>(v, yb, yo, write_y_out);
+    } else {
+        quantize_chunks<PC>(xv, nwv, scale, ys, jc, s16);
+        if (write_y_out) {
+#pragma unroll
+            for (int ci = 0; ci < PC; ++ci) {
+                const float x4[4] = {xv[ci].x, xv[ci].y, xv[ci].z, xv[ci].w};
+                quantize_chunk<true>(x4, true, scale, nwv[ci], a.y_out + (int64_t) t * a.y_out_stride,
+                                     min(p + NP * ci, nchunk - 1));
+            }
         }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");      // the row is in LDS before the count
@@ -195,7 +211,7 @@ __device__ __forceinline__ void gu_block_q8_1(const GemvArgs &a, int t, int loca
 // start, so no wave waits for another wave's weight stream.
 // Dynamic LDS: [nwaves x (up span | gate span)] [q8_1 row] [4 counters | 32 chunk sums | 32-row block |
 // 16-value sums of the row (int16)]
-template <int TW, int TS>
+template <int TW, int TS, int AQ>
 __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void mc_ffn_gate_up_kernel(const GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int NP = FFN_GU_PRO_WAVES;
@@ -220,8 +236,8 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
     lds_barrier();                                            // counters set; nothing is in flight yet
     if (wave < NP) {
         const bool y_out = a.y_out && (b % a.wg_per_tok) == 0;
-        if (a.ncols <= 4 * NP * RMS_CHUNK) gu_prologue<4>(a, t, wave, red, ys, s16, sync, y_out);
-        else gu_prologue<8192 / RMS_CHUNK / NP>(a, t, wave, red, ys, s16, sync, y_out);
+        if (a.ncols <= 4 * NP * RMS_CHUNK) gu_prologue<4, AQ>(a, t, wave, red, ys, s16, sync, y_out);
+        else gu_prologue<8192 / RMS_CHUNK / NP, AQ>(a, t, wave, red, ys, s16, sync, y_out);
         return;
     }
     const int sw = wave - NP;
@@ -258,11 +274,11 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
         float su, sg;
         if (sh) {
             if constexpr (TS != 0) {
-                step_dots<TS, ACT_Q8_1, true>(a, s, span, ys, su, sg, s16);
+                step_dots<TS, AQ, true, AQ == ACT_Q8_K ? Q8K_LDS_STRIDE : 0>(a, s, span, ys, su, sg, s16);
                 rl = step_store<TS>(a, s, su, sg, v);
             }
         } else {
-            step_dots<TW, ACT_Q8_1, true>(a, s, span, ys, su, sg, s16);
+            step_dots<TW, AQ, true, AQ == ACT_Q8_K ? Q8K_LDS_STRIDE : 0>(a, s, span, ys, su, sg, s16);
             rl = step_store<TW>(a, s, su, sg, v);
         }
     }
@@ -274,10 +290,11 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
 // down projection + combine
 // ---------------------------------------------------------------------------
 // Dynamic LDS: [nwaves x (span | activation staging | q8_1 row | 16-value sums)] [row results nwaves x rps]
-template <int TW, int TS, int ACT>
+// ACT: the routed rows' format (q8_1 or fp32); AQ: the dots' format (q8_1, or q8_K of fp32 rows)
+template <int TW, int TS, int ACT, int AQ>
 __global__ __launch_bounds__(FFN_DN_MAX_WAVES *WAVE) void mc_ffn_down_combine_kernel(const GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    constexpr int AQ = ACT == ACT_F32 ? ACT_Q8_1 : ACT;
+    static_assert(AQ == ACT_Q8_1 || ACT == ACT_F32, "q8_K dots quantize fp32 rows");
     const int wave = __builtin_amdgcn_readfirstlane((int) (threadIdx.x / WAVE)), lane = threadIdx.x % WAVE;
     if (a.rec && blockIdx.x == 0) {
         if (wave == 0) record_picks(a);
@@ -322,23 +339,24 @@ __global__ __launch_bounds__(FFN_DN_MAX_WAVES *WAVE) void mc_ffn_down_combine_ke
         wait_loads_at_most(s.n_up);
         const uint8_t *arow = span + a.lds_act + alead;
         if (qf32) {
-            quantize_row_lds((const float *) arow, span + a.lds_q8, a.ncols);
+            if constexpr (AQ == ACT_Q8_K) quantize_row_lds_q8K((const float *) arow, span + a.lds_q8, a.ncols);
+            else quantize_row_lds((const float *) arow, span + a.lds_q8, a.ncols);
             arow = span + a.lds_q8;
         }
-        // the row's 16-value code sums, once per wave (the K-quant dots' min terms)
-        static_assert(AQ == ACT_Q8_1, "down + combine reads q8_1 rows");
+        // the row's 16-value code sums, once per wave (the K-quant dots' min terms; q8_K
+        // blocks carry them)
         int16_t *rs16 = (int16_t *) (span + a.lds_sums);
-        row_sums16_lds(arow, a.ncols, rs16);
+        if constexpr (AQ == ACT_Q8_1) row_sums16_lds(arow, a.ncols, rs16);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         float su = 0.0f, sg = 0.0f;
         if (sh) {
             if constexpr (TS != 0) {
-                step_dots<TS, AQ, true>(a, s, span, arow, su, sg, rs16);
+                step_dots<TS, AQ, true, AQ == ACT_Q8_K ? Q8K_LDS_STRIDE : 0>(a, s, span, arow, su, sg, rs16);
                 nu = a.ncols / type_geom(TS).unit_elems;
             }
             v = su;
         } else {
-            step_dots<TW, AQ, true>(a, s, span, arow, su, sg, rs16);
+            step_dots<TW, AQ, true, AQ == ACT_Q8_K ? Q8K_LDS_STRIDE : 0>(a, s, span, arow, su, sg, rs16);
             nu = a.ncols / type_geom(TW).unit_elems;
             const int rl = lane / nu;
             v = routed_value(a, s, s.row0 + (rl < s.nrows_here ? rl : 0), su, sg);
@@ -376,23 +394,26 @@ static hipError_t launch_big_lds(K kernel, unsigned grid, unsigned block, uint32
     return hipGetLastError();
 }
 
-template <int TW, int TS>
+template <int TW, int TS, int AQ>
 static hipError_t launch_gu_t(const GemvArgs &a, hipStream_t s) {
-    return launch_big_lds(mc_ffn_gate_up_kernel<TW, TS>, (unsigned) (a.rec + a.n_tok * a.wg_per_tok),
+    return launch_big_lds(mc_ffn_gate_up_kernel<TW, TS, AQ>, (unsigned) (a.rec + a.n_tok * a.wg_per_tok),
                           (unsigned) ((a.nwaves + FFN_GU_PRO_WAVES) * WAVE), a.lds_total, a, s);
 }
 
-template <int TW, int TS, int ACT>
+template <int TW, int TS, int ACT, int AQ>
 static hipError_t launch_dn_t(const GemvArgs &a, hipStream_t s) {
-    return launch_big_lds(mc_ffn_down_combine_kernel<TW, TS, ACT>, (unsigned) (a.rec + a.n_tok * a.wg_per_tok),
+    return launch_big_lds(mc_ffn_down_combine_kernel<TW, TS, ACT, AQ>, (unsigned) (a.rec + a.n_tok * a.wg_per_tok),
                           (unsigned) (a.nwaves * WAVE), a.lds_total, a, s);
 }
 
 template <int TW, int TS>
 static hipError_t launch_mode(const GemvArgs &a, int act, hipStream_t s) {
-    if (a.mode == FFN_GATE_UP_NORM) return launch_gu_t<TW, TS>(a, s);
-    if (act == ACT_F32) return launch_dn_t<TW, TS, ACT_F32>(a, s);
-    return launch_dn_t<TW, TS, ACT_Q8_1>(a, s);
+    const bool q8k = a.dot_act == ACT_Q8_K;
+    if (a.mode == FFN_GATE_UP_NORM)
+        return q8k ? launch_gu_t<TW, TS, ACT_Q8_K>(a, s) : launch_gu_t<TW, TS, ACT_Q8_1>(a, s);
+    if (q8k) return act == ACT_F32 ? launch_dn_t<TW, TS, ACT_F32, ACT_Q8_K>(a, s) : hipErrorInvalidValue;
+    if (act == ACT_F32) return launch_dn_t<TW, TS, ACT_F32, ACT_Q8_1>(a, s);
+    return launch_dn_t<TW, TS, ACT_Q8_1, ACT_Q8_1>(a, s);
 }
 
 template <int TW>
@@ -412,7 +433,7 @@ static uint32_t round16(uint32_t b) { return (b + 15u) & ~15u; }
 
 // Tiling and LDS layout of the fused kernels; returns hipErrorInvalidValue when
 // the shape does not fit (the host validated types and alignment).
-static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act) {
+static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act, int n_cu) {
     const TypeGeom g = type_geom(tw);
     const int nu = a.ncols / g.unit_elems;
     const uint32_t rb = (uint32_t) nu * (uint32_t) g.unit_bytes;
@@ -422,8 +443,9 @@ static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act) {
     a.rec = (a.stats || a.stamps || a.stamps_gate) ? 1 : 0;
     if (a.mode == FFN_GATE_UP_NORM) {
         if (a.ncols % RMS_CHUNK || a.ncols > 8192) return hipErrorInvalidValue;
-        const uint32_t common = round16((uint32_t) (a.ncols / 32 * 36)) + 16u + 4u * 32u + 4u * 32u +
-                                2u * (uint32_t) (a.ncols / 16);
+        // the normalized row: q8_1 blocks, or q8_K blocks (one per 256 values) for q8_K dots
+        const uint32_t yrow = a.dot_act == ACT_Q8_K ? (uint32_t) (a.ncols / 256 * Q8K_LDS_STRIDE) : (uint32_t) (a.ncols / 32 * 36);
+        const uint32_t common = round16(yrow) + 16u + 4u * 32u + 4u * 32u + 2u * (uint32_t) (a.ncols / 16);
         int rps, sh_rps;
         if (a.hq) {
             // workgroups of exactly one q8_1 block of rows: steps of a power-of-two row count
@@ -446,9 +468,22 @@ static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act) {
             a.sh_tiles_per_tok = ts ? (a.nrows + sh_rps - 1) / sh_rps : 0;
             a.tiles_per_tok = a.sh_tiles_per_tok + a.n_used * a.tiles_per_pick;
             if (!a.hq) {
-                // as many step waves per workgroup as fill about one workgroup per CU
-                const int want = (a.tiles_per_tok * a.n_tok + 255) / 256;
-                a.nwaves = want < 1 ? 1 : (want > FFN_GU_MAX_WAVES ? FFN_GU_MAX_WAVES : want);
+                // routed steps per workgroup: about the launch's bytes per CU (one workgroup per CU,
+                // every workgroup resident at once), the shared matrix in workgroups of at most as
+                // many bytes (sh_per_wg below)
+                const double rstep = (double) rps * rb, sstep = ts ? (double) sh_rps * rbs : 1.0;
+                const double total = (double) a.n_tok * ((double) a.n_used * a.tiles_per_pick * rstep +
+                                                         (double) a.sh_tiles_per_tok * sstep);
+                int nw = (int) (total / n_cu / rstep) + 1;
+                nw = nw < 1 ? 1 : (nw > FFN_GU_MAX_WAVES ? FFN_GU_MAX_WAVES : nw);
+                for (; nw < FFN_GU_MAX_WAVES; ++nw) {
+                    int shw = ts ? (int) (nw * rstep / sstep) : 0;
+                    shw = !ts ? 0 : (shw < 1 ? 1 : (shw > nw ? nw : shw));
+                    const int wgs = a.n_tok * ((shw ? (a.sh_tiles_per_tok + shw - 1) / shw : 0) +
+                                               (a.n_used * a.tiles_per_pick + nw - 1) / nw);
+                    if (wgs <= n_cu) break;
+                }
+                a.nwaves = nw;
             }
             // spans sized to the 16-byte chunk the DMA writes last (+ lead-in and over-read)
             const uint32_t sr = round16((uint32_t) rps * rb + 20u);
@@ -475,7 +510,7 @@ static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act) {
         const int nsh_wg = a.sh_per_wg ? (a.sh_tiles_per_tok + a.sh_per_wg - 1) / a.sh_per_wg : 0;
         a.wg_per_tok = nsh_wg + (a.tiles_per_tok - a.sh_tiles_per_tok + a.nwaves - 1) / a.nwaves;
         a.lds_y = (uint32_t) a.nwaves * a.lds_wave;
-        a.lds_part = a.lds_y + round16((uint32_t) (a.ncols / 32 * 36));
+        a.lds_part = a.lds_y + round16(yrow);
         a.lds_total = a.lds_part + 16u + 4u * 32u + 4u * 32u + 2u * (uint32_t) (a.ncols / 16);
         a.n_tiles = a.tiles_per_tok * a.n_tok;
         return hipSuccess;
@@ -488,7 +523,8 @@ static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act) {
     // enough workgroups for every CU: at most nrows * n_tok / 256 rows each
     const int fill = (a.nrows * a.n_tok + 255) / 256;
     if (fill < rps) rps = fill < 1 ? 1 : fill;
-    const uint32_t q8_bytes = act == ACT_F32 || (ts && a.sh_act_f32) ? round16((uint32_t) (a.ncols / 32 * 36)) : 0u;
+    const uint32_t q8_row = a.dot_act == ACT_Q8_K ? (uint32_t) (a.ncols / 256 * Q8K_LDS_STRIDE) : (uint32_t) (a.ncols / 32 * 36);
+    const uint32_t q8_bytes = act == ACT_F32 || (ts && a.sh_act_f32) ? round16(q8_row) : 0u;
     const uint32_t arow_max = ts && a.sh_act_row_bytes > a.act_row_bytes ? a.sh_act_row_bytes : a.act_row_bytes;
     for (;;) {
         const uint32_t sr = span_bytes((uint32_t) rps, rb);
@@ -514,6 +550,21 @@ static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act) {
     return hipSuccess;
 }
 
+// Compute units of the current GPU (looked up once per GPU; 256 when the query fails).
+static int cu_count() {
+    static std::mutex m;
+    static int cache[MAX_DEVICES] = {};
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= MAX_DEVICES) return 256;
+    std::lock_guard<std::mutex> lock(m);
+    if (!cache[d]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, d) != hipSuccess || n <= 0) n = 256;
+        cache[d] = n;
+    }
+    return cache[d];
+}
+
 // Fused decode launch (a.mode != FFN_NONE): tiling, LDS layout, dispatch on the
 // routed type (K-quants) and the shared-expert type (none or a K-quant).
 int launch_ffn(GemvArgs a, int tw, int ts, int act, void *stream) {
@@ -521,7 +572,7 @@ int launch_ffn(GemvArgs a, int tw, int ts, int act, void *stream) {
     if (a.mode == FFN_GATE_UP_NORM) act = ACT_Q8_1;
     a.act_row_bytes = act == ACT_Q8_1 ? (uint32_t) (a.ncols / 32 * 36) : (uint32_t) a.ncols * 4u;
     a.sh_act_row_bytes = act == ACT_Q8_1 && !a.sh_act_f32 ? (uint32_t) (a.ncols / 32 * 36) : (uint32_t) a.ncols * 4u;
-    hipError_t err = ffn_layout(a, tw, ts, act);
+    hipError_t err = ffn_layout(a, tw, ts, act, cu_count());
     if (err != hipSuccess) return (int) err;
     if (a.n_tiles <= 0) return (int) hipSuccess;
     hipStream_t s = (hipStream_t) stream;

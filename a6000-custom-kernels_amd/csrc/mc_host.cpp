@@ -499,6 +499,7 @@ struct FfnExtra {
     float *x_out = nullptr;
     int64_t x_stride = 0;
     bool sh_act_f32 = false;         // FFN_DOWN_COMBINE: the shared expert's rows are fp32
+    int dot_act = ACT_Q8_1;          // the dots' activation format (ACT_Q8_1 or ACT_Q8_K)
 };
 
 // Shared validation + launch of the GEMV (and of the fused decode kernels when fx is given).
@@ -668,6 +669,7 @@ int gemv_common(int use_cache, int act, const ggml_hip_moe_tensor *src0, const g
         a.hq_stride_pick = fx->hq_stride_pick;
         a.hq_sh = fx->hq_sh;
         a.hq_sh_stride = fx->hq_sh_stride;
+        a.dot_act = fx->dot_act;
         a.router_w = fx->router_w;
         a.residual = fx->residual;
         a.x_out = fx->x_out;
@@ -936,7 +938,26 @@ int ggml_hip_moe_ffn_gate_up_norm(int use_cache, const ggml_hip_moe_tensor *src0
                                   int64_t stride_channel_dst, int64_t ids_stride, void *y_out, int64_t y_out_stride,
                                   void *dst_q8_1, int64_t q8_stride_col, int64_t q8_stride_channel,
                                   void *shared_dst_q8_1, int64_t shared_q8_stride_col, void *stream) {
+    return ggml_hip_moe_ffn_gate_up_norm_ex(use_cache, ACT_Q8_1, src0, gate_host, fusion, x, norm_weight, eps, ids_d, dst_d,
+                                            ne00, ne01, ne02, ncols_dst, nchannels_dst, stride_col_x, stride_col_dst,
+                                            stride_channel_dst, ids_stride, y_out, y_out_stride, dst_q8_1, q8_stride_col,
+                                            q8_stride_channel, shared_dst_q8_1, shared_q8_stride_col, stream);
+}
+
+int ggml_hip_moe_ffn_gate_up_norm_ex(int use_cache, int act_format, const ggml_hip_moe_tensor *src0,
+                                     const ggml_hip_moe_tensor *gate_host, const ggml_hip_moe_fusion *fusion, const float *x,
+                                     const float *norm_weight, float eps, const int32_t *ids_d, float *dst_d, int64_t ne00,
+                                     int64_t ne01, int64_t ne02, int64_t ncols_dst, int64_t nchannels_dst,
+                                     int64_t stride_col_x, int64_t stride_col_dst, int64_t stride_channel_dst,
+                                     int64_t ids_stride, void *y_out, int64_t y_out_stride, void *dst_q8_1,
+                                     int64_t q8_stride_col, int64_t q8_stride_channel, void *shared_dst_q8_1,
+                                     int64_t shared_q8_stride_col, void *stream) {
     if (!x) return fail(E_INVALID, "moe-ffn: null x");
+    if (act_format != ACT_Q8_1 && act_format != ACT_Q8_K)
+        return fail(E_UNSUPPORTED, "moe-ffn: the normalized row is q8_1 or q8_K (act_format %d)", act_format);
+    const bool q8k = act_format == ACT_Q8_K;
+    if (q8k && (dst_q8_1 || shared_dst_q8_1))
+        return fail(E_UNSUPPORTED, "moe-ffn: q8_K dots write fp32 outputs only (the down launch quantizes them)");
     if (dst_q8_1) {
         if (ne01 % 32) return fail(E_UNSUPPORTED, "moe-ffn: q8_1 outputs need ne01 %% 32 == 0");
         if (ne00 / 256 > 16) return fail(E_UNSUPPORTED, "moe-ffn: q8_1 outputs need at most 16 units per row");
@@ -949,7 +970,7 @@ int ggml_hip_moe_ffn_gate_up_norm(int use_cache, const ggml_hip_moe_tensor *src0
     if ((((uintptr_t) x) & 15u) || (stride_col_x & 3) || (ncols_dst > 1 && stride_col_x < ne00))
         return fail(E_INVALID, "moe-ffn: x rows must be 16-byte aligned and not overlap");
     if (norm_weight && (((uintptr_t) norm_weight) & 15u)) return fail(E_INVALID, "moe-ffn: norm_weight must be 16-byte aligned");
-    if (y_out && ((((uintptr_t) y_out) & 3u) || (ncols_dst > 1 && y_out_stride < ne00 / 32)))
+    if (y_out && ((((uintptr_t) y_out) & 3u) || (ncols_dst > 1 && y_out_stride < ne00 / (q8k ? 256 : 32))))
         return fail(E_INVALID, "moe-ffn: y_out rows must be 4-byte aligned and not overlap");
     if (fusion && fusion->shared_src1) return fail(E_INVALID, "moe-ffn: the shared expert reads the normalized row (shared_src1 must be NULL)");
     FfnExtra fx;
@@ -959,7 +980,8 @@ int ggml_hip_moe_ffn_gate_up_norm(int use_cache, const ggml_hip_moe_tensor *src0
     fx.nw = norm_weight;
     fx.eps = eps;
     fx.y_out = (uint8_t *) y_out;
-    fx.y_out_stride = y_out_stride * 36;
+    fx.y_out_stride = y_out_stride * (q8k ? 292 : 36);
+    fx.dot_act = q8k ? ACT_Q8_K : ACT_Q8_1;
     fx.hq = (uint8_t *) dst_q8_1;
     fx.hq_stride_col = q8_stride_col * 36;
     fx.hq_stride_pick = q8_stride_channel * 36;
@@ -978,8 +1000,10 @@ int ggml_hip_moe_ffn_down_combine(int use_cache, int act_format, const ggml_hip_
     if (!router_w || !x_out) return fail(E_INVALID, "moe-ffn: null router weights or x_out");
     if (use_cache && !wants_impl(src0)) return fail(E_STATE, "moe-cache: src0 does not qualify for the cache path (wants() == 0)");
     const bool sh_f32 = (act_format & GGML_HIP_MOE_ACT_SHARED_F32) != 0;
-    act_format &= ~GGML_HIP_MOE_ACT_SHARED_F32;
+    const bool dot_q8k = (act_format & GGML_HIP_MOE_ACT_DOT_Q8_K) != 0;
+    act_format &= ~(GGML_HIP_MOE_ACT_SHARED_F32 | GGML_HIP_MOE_ACT_DOT_Q8_K);
     if (act_format != ACT_Q8_1 && act_format != ACT_F32) return fail(E_UNSUPPORTED, "moe-ffn: down activations are q8_1 or fp32 rows");
+    if (dot_q8k && act_format != ACT_F32) return fail(E_UNSUPPORTED, "moe-ffn: q8_K dots quantize fp32 rows (act_format F32)");
     if (fusion && (fusion->gate || fusion->shared_gate || fusion->gate_bias || fusion->gate_scale))
         return fail(E_INVALID, "moe-ffn: the down projection takes no gate");
     if (fusion && fusion->shared_up && !fusion->shared_src1) return fail(E_INVALID, "moe-ffn: shared expert without its activation row (shared_src1)");
@@ -988,6 +1012,7 @@ int ggml_hip_moe_ffn_down_combine(int use_cache, int act_format, const ggml_hip_
     FfnExtra fx;
     fx.mode = FFN_DOWN_COMBINE;
     fx.sh_act_f32 = sh_f32 || act_format == ACT_F32;
+    fx.dot_act = dot_q8k ? ACT_Q8_K : ACT_Q8_1;
     fx.router_w = router_w;
     fx.residual = residual;
     fx.x_out = x_out;

@@ -133,6 +133,7 @@ struct GemvArgs {
     // fused decode kernels (mc_ffn.hip); FFN_NONE: the plain MUL_MAT_ID GEMV
     int32_t mode;
     int32_t nwaves;               // step waves per workgroup (FFN_GATE_UP_NORM: plus FFN_GU_PRO_WAVES)
+    int32_t dot_act;              // fused kernels: the dots' activation format (ACT_Q8_1 or ACT_Q8_K)
     int32_t sh_per_wg;            // FFN_GATE_UP_NORM: steps of a shared-expert workgroup (its first
                                   //   workgroups take only shared steps, about as many bytes as the
                                   //   routed workgroups' nwaves steps)

@@ -183,12 +183,13 @@ __device__ __forceinline__ void step_issue(const GemvArgs &a, StepCtx &s, uint8_
 // blocks) is in LDS at arow and, when there is a gate, the gate span has landed
 // (the caller waited for at most n_up outstanding loads); the up span is waited
 // for here.  Returns the row sums (valid in lane row_local * nu of each row).
-template <int T, int AQ, bool S16 = false>
+template <int T, int AQ, bool S16 = false, int ASTRIDE = 0>
 __device__ __forceinline__ void step_dots(const GemvArgs &a, const StepCtx &s, const uint8_t *span,
                                           const uint8_t *arow, float &su, float &sg, const int16_t *s16 = nullptr) {
     constexpr TypeGeom G = type_geom(T);
     constexpr int UE = G.unit_elems;
-    constexpr int AUB = AQ == ACT_Q8_1 ? UE / 32 * 36 : 292;     // activation bytes per unit
+    // activation bytes per unit in the row (ASTRIDE: a padded LDS layout)
+    constexpr int AUB = ASTRIDE ? ASTRIDE : AQ == ACT_Q8_1 ? UE / 32 * 36 : 292;
     const int lane = threadIdx.x % WAVE;
     const int nu = a.ncols / UE;
     const int row_local = lane / nu, col = lane % nu;
@@ -198,7 +199,8 @@ __device__ __forceinline__ void step_dots(const GemvArgs &a, const StepCtx &s, c
     Act<UE> A;
     float pu = 0.0f, pg = 0.0f;
     // precomputed 16-value activation sums of the unit, when the caller has them (K-quant units)
-    const int16_t *us16 = S16 ? s16 + (u32) col * (UE / 16) : nullptr;
+    // (q8_K units carry their own bsums)
+    const int16_t *us16 = S16 && AQ != ACT_Q8_K ? s16 + (u32) col * (UE / 16) : nullptr;
     if (s.wgate) {
         if (active) {
             load_act_lds<UE, AQ, S16>(A, aslice, us16);

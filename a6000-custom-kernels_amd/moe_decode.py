@@ -34,7 +34,7 @@ import math
 
 import numpy as np
 
-from . import (ACT_F32, ACT_Q8_1, ACT_SHARED_F32, BLOCK, GLU_SWIGLU, KQUANTS, Q2_K, Q3_K, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0, check,
+from . import (ACT_DOT_Q8_K, ACT_F32, ACT_Q8_1, ACT_Q8_K, ACT_SHARED_F32, BLOCK, GLU_SWIGLU, KQUANTS, Q2_K, Q3_K, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0, check,
                lib, make_fusion, make_tensor, row_bytes)
 
 # byte offsets of the fp16 block-scale fields per type, and the value written there
@@ -69,9 +69,13 @@ class Layer:
 
 class MoeDecodeModel:
     def __init__(self, torch, n_layers=48, n_experts=512, hidden=4096, ffn=768, n_used=8, wtype=Q2_K,
-                 sh_type=Q4_K, seed=0, device="cuda", residual=True, fused=True, shared_q8=True):
+                 sh_type=Q4_K, seed=0, device="cuda", residual=True, fused=True, shared_q8=True, act="q8_1"):
         self.torch = torch
         self.fused = fused
+        # fused plan: the dots run on q8_1 rows (ggml-CUDA's MMVQ activations, the reference's
+        # path) or on q8_K rows (ggml-CPU's MUL_MAT_ID activations for K-quant experts)
+        assert act in ("q8_1", "q8_K") and (act == "q8_1" or fused)
+        self.act = act
         # fused plan: the gate/up launch writes the shared expert's q8_1 row (32-row shared
         # workgroups) or only its fp32 row, which the down launch quantizes (shared
         # workgroups of a routed one's bytes)
@@ -122,15 +126,20 @@ class MoeDecodeModel:
     def gate_up_bytes(self):
         H, F, U = self.H, self.F, self.U
         w = U * 2 * row_bytes(self.wtype, H) * F + 2 * row_bytes(self.sh_type, H) * F
-        if self.fused:                                 # x row + norm weight in, GLU rows (fp32 + routed q8_1) out
-            return w + 2 * H * 4 + (U + 1) * F * 4 + U * F // 32 * 36
+        if self.fused and self.act == "q8_K":          # x row + norm weight in, fp32 GLU rows out
+            return w + 2 * H * 4 + (U + 1) * F * 4
+        if self.fused:                                 # x row + norm weight in, GLU rows (fp32 + q8_1) out
+            return w + 2 * H * 4 + (U + 1) * F * 4 + (U + 1 if self.shared_q8 else U) * F // 32 * 36
         return w + H // 32 * 36 + (U + 1) * F * 4      # q8_1 row in, GLU rows out
 
     def down_bytes(self):
         H, F, U = self.H, self.F, self.U
         w = U * row_bytes(self.wtype, F) * H + row_bytes(self.sh_type, F) * H
-        if self.fused:                                 # routed q8_1 + shared fp32 GLU rows, residual, router weights in; x out
-            return w + U * F // 32 * 36 + F * 4 + 2 * H * 4 + U * 4
+        if self.fused and self.act == "q8_K":          # fp32 GLU rows, residual, router weights in; x out
+            return w + (U + 1) * F * 4 + 2 * H * 4 + U * 4
+        if self.fused:                                 # q8_1 (+ fp32 shared) GLU rows, residual, router weights in; x out
+            sh_in = F // 32 * 36 if self.shared_q8 else F * 4
+            return w + U * F // 32 * 36 + sh_in + 2 * H * 4 + U * 4
         return w + (U + 1) * F * 4 + (U + 1) * H * 4   # GLU rows in, expert outputs out
 
     def combine_bytes(self):
@@ -178,6 +187,13 @@ class MoeDecodeModel:
         s = s or self._stream()
         H, F, U = self.H, self.F, self.U
         nb = F // 32
+        if self.act == "q8_K":
+            check(lib().ggml_hip_moe_ffn_gate_up_norm_ex(0, ACT_Q8_K, C.byref(ly.t_up), None, C.byref(ly.f_gu),
+                                                         src.data_ptr(), self.norm[l].data_ptr(), self.eps,
+                                                         self.ids[l].data_ptr(), self.h.data_ptr(), H, F, self.E, 1, U,
+                                                         H, U * F, F, U, None, 0, None, 0, 0, None, 0, s),
+                  "gate_up_norm q8_K")
+            return
         check(lib().ggml_hip_moe_ffn_gate_up_norm(0, C.byref(ly.t_up), None, C.byref(ly.f_gu), src.data_ptr(),
                                                   self.norm[l].data_ptr(), self.eps, self.ids[l].data_ptr(),
                                                   self.h.data_ptr(), H, F, self.E, 1, U, H, U * F, F, U, None, 0,
@@ -192,6 +208,13 @@ class MoeDecodeModel:
         s = s or self._stream()
         H, F, U = self.H, self.F, self.U
         nb = F // 32
+        if self.act == "q8_K":                         # fp32 GLU rows, quantized to q8_K by each wave
+            check(lib().ggml_hip_moe_ffn_down_combine(0, ACT_F32 | ACT_DOT_Q8_K, C.byref(ly.t_down), C.byref(ly.f_dn),
+                                                      self.h.data_ptr(), self.ids[l].data_ptr(), self.w[l].data_ptr(),
+                                                      src.data_ptr() if self.residual else None, dst.data_ptr(),
+                                                      F, H, self.E, 1, U, (U + 1) * F, F, H, U, s),
+                  "down_combine q8_K")
+            return
         act = ACT_Q8_1 if self.shared_q8 else ACT_Q8_1 | ACT_SHARED_F32
         check(lib().ggml_hip_moe_ffn_down_combine(0, act, C.byref(ly.t_down),
                                                   C.byref(ly.f_dnq if self.shared_q8 else ly.f_dn),

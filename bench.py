@@ -453,6 +453,9 @@ def main():
     ap.add_argument("--shared-rows", choices=("q8_1", "f32"), default="q8_1",
                     help="fused plan: the gate/up launch writes the shared expert's q8_1 row (q8_1), or only its "
                          "fp32 row, quantized by the down launch, with byte-balanced shared workgroups (f32)")
+    ap.add_argument("--act", choices=("q8_1", "q8_K"), default="q8_1",
+                    help="fused plan: the dots' activations, q8_1 (ggml-CUDA MMVQ, the reference's path) or q8_K "
+                         "(ggml-CPU MUL_MAT_ID for K-quant experts)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: a 1 GiB copy (the counter calibration) and the gate/up "
                          "GEMV of every layer, then exit")
@@ -486,7 +489,8 @@ def main():
         return
     t0 = time.perf_counter()
     fused = args.plan == "fused"
-    model = md.MoeDecodeModel(torch, n_layers=args.layers, fused=fused, shared_q8=args.shared_rows == "q8_1")
+    model = md.MoeDecodeModel(torch, n_layers=args.layers, fused=fused, shared_q8=args.shared_rows == "q8_1",
+                              act=args.act if fused else "q8_1")
     torch.cuda.synchronize()
     log(f"weights ready: {args.layers} layers in {time.perf_counter() - t0:.1f}s, "
         f"{torch.cuda.memory_allocated() / 2**30:.1f} GiB allocated")
@@ -537,6 +541,40 @@ def main():
     log(f"gate/up: {gu_ms * 1000:.2f} us/launch ({n_launch} launches), {gu_gbs:.0f} GB/s; "
         f"down: {dn_ms * 1000:.2f} us/launch, {dn_gbs:.0f} GB/s")
 
+    # the other activation format of the fused plan, on the same weights and routes
+    modes = {}
+    if fused:
+        main_act = model.act
+        for act in ("q8_1", "q8_K"):
+            if act == main_act:
+                continue
+            model.act = act
+            model.x.copy_(x0)
+            model.set_routing(ids_dev[0], w_dev[0])
+            model.capture()
+            for i in range(args.warmup):
+                model.set_routing(ids_dev[i % n_tok_routes], w_dev[i % n_tok_routes])
+                model.replay()
+            n2 = max(1, args.steps // 2)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for i in range(n2):
+                j = (args.warmup + i) % n_tok_routes
+                model.set_routing(ids_dev[j], w_dev[j])
+                model.replay()
+            e1.record(s)
+            torch.cuda.synchronize()
+            ms2 = e0.elapsed_time(e1) / n2
+            g2, _ = time_kernel(torch, model, gate_up_launcher(model), args.kernel_rounds)
+            d2, _ = time_kernel(torch, model, down_launcher(model), args.kernel_rounds)
+            modes[act] = {"ms_per_step": round(ms2, 4), "tok_per_s": round(1000.0 / ms2, 2), "steps": n2,
+                          "gate_up_us_per_launch": round(g2 * 1000, 3), "down_us_per_launch": round(d2 * 1000, 3),
+                          "gate_up_bytes_per_launch": model.gate_up_bytes(),
+                          "down_bytes_per_launch": model.down_bytes()}
+            log(f"{act} activations: {ms2 * 1000:.1f} us/token, gate/up {g2 * 1000:.2f} us, down {d2 * 1000:.2f} us")
+        model.act = main_act
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(torch, model, ids_np, w_np)
@@ -561,7 +599,7 @@ def main():
                    "layers": model.L, "experts": model.E, "hidden": model.H, "ffn": model.F, "top_k": model.U,
                    "routed_type": "q2_K", "shared_type": "q4_K", "batch": 1,
                    "plan": f"{args.plan}: {2 if fused else 3} launches per layer",
-                   "shared_rows": args.shared_rows},
+                   "shared_rows": args.shared_rows, "activations": model.act},
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "tok_per_s": round(tok_s, 2),
         "bytes_per_step": bpt,
@@ -573,6 +611,8 @@ def main():
                              "us_per_launch": round(dn_ms * 1000, 3), "GB/s": round(dn_gbs, 1)}},
         "cpu_baseline": cpu,
     }
+    if modes:
+        out["other_activation_modes"] = modes
     if wl_names:
         del model                             # 71 GiB of decode weights are not needed below
         torch.cuda.empty_cache()

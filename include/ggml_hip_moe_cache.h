@@ -78,8 +78,11 @@ enum {
     GGML_HIP_MOE_ACT_Q8_K = 1, /* ggml-CPU q8_K blocks (292 B / 256 values), K-quant weights only */
     GGML_HIP_MOE_ACT_F32  = 2, /* fp32 rows, quantized to q8_1 inside the GEMV with the codes and
                                   scales ggml_hip_quantize_q8_1 produces (fuses that launch away) */
-    GGML_HIP_MOE_ACT_SHARED_F32 = 0x100  /* ggml_hip_moe_ffn_down_combine flag: the shared
+    GGML_HIP_MOE_ACT_SHARED_F32 = 0x100, /* ggml_hip_moe_ffn_down_combine flag: the shared
                                             expert's rows are fp32 (quantized in the launch) */
+    GGML_HIP_MOE_ACT_DOT_Q8_K = 0x200    /* ggml_hip_moe_ffn_down_combine flag (with F32 rows):
+                                            the rows are quantized to q8_K, as ggml-CPU's
+                                            MUL_MAT_ID does for K-quant experts */
 };
 
 /* POD mirror of the ggml_tensor fields the path reads
@@ -255,6 +258,21 @@ int ggml_hip_moe_combine_q8_1(const float *o, int64_t o_stride, const float *w, 
  * row itself (GGML_HIP_MOE_ACT_SHARED_F32). */
 int ggml_hip_moe_ffn_gate_up_norm(
         int use_cache, const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *gate_host,
+        const ggml_hip_moe_fusion *fusion, const float *x, const float *norm_weight, float eps,
+        const int32_t *ids_d, float *dst_d, int64_t ne00, int64_t ne01, int64_t ne02,
+        int64_t ncols_dst, int64_t nchannels_dst, int64_t stride_col_x, int64_t stride_col_dst,
+        int64_t stride_channel_dst, int64_t ids_stride, void *y_out, int64_t y_out_stride,
+        void *dst_q8_1, int64_t q8_stride_col, int64_t q8_stride_channel,
+        void *shared_dst_q8_1, int64_t shared_q8_stride_col, void *stream);
+
+/* ggml_hip_moe_ffn_gate_up_norm with the normalized row in act_format:
+ * GGML_HIP_MOE_ACT_Q8_1 (as above), or GGML_HIP_MOE_ACT_Q8_K: y[t] is quantized to q8_K
+ * blocks (ggml-CPU's quantize_row_q8_K_ref on the same fp32 values) and every dot runs on
+ * them, as ggml-CPU's MUL_MAT_ID does for K-quant experts; y_out then receives q8_K rows
+ * (y_out_stride in 292-byte blocks) and dst_q8_1 / shared_dst_q8_1 must be NULL (the down
+ * launch quantizes the fp32 outputs itself: GGML_HIP_MOE_ACT_F32 | GGML_HIP_MOE_ACT_DOT_Q8_K). */
+int ggml_hip_moe_ffn_gate_up_norm_ex(
+        int use_cache, int act_format, const ggml_hip_moe_tensor *src0, const ggml_hip_moe_tensor *gate_host,
         const ggml_hip_moe_fusion *fusion, const float *x, const float *norm_weight, float eps,
         const int32_t *ids_d, float *dst_d, int64_t ne00, int64_t ne01, int64_t ne02,
         int64_t ncols_dst, int64_t nchannels_dst, int64_t stride_col_x, int64_t stride_col_dst,

@@ -388,3 +388,187 @@ def test_gate_up_norm_timeout_reports_status(torch_gpu, mc):
                    n_experts=E, fusion=f)
     torch.cuda.synchronize()
     assert torch.equal(dst, dst_ref)
+
+
+# ---------------------------------------------------------------------------
+# q8_K mode: the dots on q8_K rows (ggml-CPU's MUL_MAT_ID activations for K-quant experts)
+# ---------------------------------------------------------------------------
+
+def _normalized(O, x, nw, eps):
+    """(x * s) * nw with s = 1/sqrt(mean(x^2) + eps), the mean of squares in the canonical order."""
+    K = x.shape[-1]
+    out = np.empty_like(x)
+    for t in range(x.shape[0]):
+        ss = np.float32(O.rms_sum(x[t]))
+        s = np.float32(1.0) / np.sqrt(ss / np.float32(K) + np.float32(eps))
+        v = (x[t] * s).astype(np.float32)
+        out[t] = (v * nw).astype(np.float32) if nw is not None else v
+    return out
+
+
+@pytest.mark.parametrize("wtype,sh_type,K,R,n_tok,with_nw,bad_id", [
+    ("Q2_K", "Q4_K", 4096, 768, 1, True, False),
+    ("Q2_K", "Q4_K", 2048, 96, 3, True, True),
+    ("Q4_K", "Q6_K", 1024, 160, 2, False, False),
+    ("Q3_K", None, 1024, 128, 1, True, False),
+    ("Q5_K", "Q2_K", 8192, 64, 1, True, False),
+])
+def test_gate_up_norm_q8K(torch_gpu, mc, O, wtype, sh_type, K, R, n_tok, with_nw, bad_id):
+    """q8_K rows: y_out byte-identical to the oracle's q8_K of the normalized row, the outputs
+    bit-identical to the q8_K GEMV on those rows and within fp32 summation order of the oracle."""
+    torch = torch_gpu
+    md = import_module("a6000_custom_kernels_amd.moe_decode")
+    _note(f"gate_up_norm q8_K {wtype}/{sh_type} K={K} R={R} tok={n_tok} nw={with_nw} bad_id={bad_id}")
+    E, U, eps = 16, 4, 1e-6
+    tw = getattr(mc, wtype)
+    ts = getattr(mc, sh_type) if sh_type else None
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(K + R + n_tok + 1)
+    up = md.random_expert_tensor(torch, tw, E, R, K, gen)
+    gate = md.random_expert_tensor(torch, tw, E, R, K, gen)
+    sh_up = md.random_expert_tensor(torch, ts, 1, R, K, gen)[0] if ts else None
+    sh_gate = md.random_expert_tensor(torch, ts, 1, R, K, gen)[0] if ts else None
+    rng = np.random.default_rng(K * 5 + n_tok)
+    x_np = (rng.standard_normal((n_tok, K)) * 3).astype(np.float32)
+    nw_np = rng.uniform(0.5, 1.5, K).astype(np.float32) if with_nw else None
+    ids_np = np.stack([rng.choice(E, U, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    if bad_id:
+        ids_np[-1, 2] = E + 5
+    x, ids = torch.from_numpy(x_np).cuda(), torch.from_numpy(ids_np).cuda()
+    nw = torch.from_numpy(nw_np).cuda() if with_nw else None
+
+    dst = torch.full((n_tok, U, R), SENTINEL, dtype=torch.float32, device="cuda")
+    sh = torch.full((n_tok, R), SENTINEL, dtype=torch.float32, device="cuda")
+    y_out = torch.zeros((n_tok, K // 256 * 292), dtype=torch.uint8, device="cuda")
+    f = mc.make_fusion(gate=gate, glu_op=mc.GLU_SWIGLU, shared_up=sh_up, shared_gate=sh_gate,
+                       shared_dst=sh if ts else None, shared_type=ts if ts else -1)
+    mc.ffn_gate_up_norm(wtype=tw, weights=up, ids=ids, x=x, dst=dst, K=K, R=R, n_experts=E, norm_weight=nw, eps=eps,
+                        fusion=f, y_out=y_out, act=mc.ACT_Q8_K)
+    torch.cuda.synchronize()
+    want_y = np.stack([O.quantize_q8_K(r) for r in _normalized(O, x_np, nw_np, eps)])
+    assert np.array_equal(y_out.cpu().numpy(), want_y)
+
+    # the q8_K GEMV on the same rows: bit-identical
+    dst_ref = torch.full((n_tok, U, R), SENTINEL, dtype=torch.float32, device="cuda")
+    sh_ref = torch.full((n_tok, R), SENTINEL, dtype=torch.float32, device="cuda")
+    f_ref = mc.make_fusion(gate=gate, glu_op=mc.GLU_SWIGLU, shared_up=sh_up, shared_gate=sh_gate,
+                           shared_dst=sh_ref if ts else None, shared_type=ts if ts else -1)
+    mc.mul_mat_vec(wtype=tw, weights=up, ids=ids, y=y_out.view(n_tok, 1, -1), dst=dst_ref, K=K, R=R, n_experts=E,
+                   act=mc.ACT_Q8_K, fusion=f_ref)
+    torch.cuda.synchronize()
+    assert torch.equal(dst, dst_ref)
+    if ts:
+        assert torch.equal(sh, sh_ref)
+    # and the oracle
+    ok = ids_np >= 0
+    ok &= ids_np < E
+    got = dst.cpu().numpy()
+    kw = dict(sh_type=ts, sh_up=sh_up.cpu().numpy(), sh_gate=sh_gate.cpu().numpy()) if ts else {}
+    res = O.mul_mat_id(wtype=tw, K=K, R=R, n_as=E, src0=up.cpu().numpy(), gate=gate.cpu().numpy(),
+                       ids=np.where(ok, ids_np, 0).astype(np.int32), act=want_y.reshape(n_tok, 1, -1),
+                       act_kind=O.ACT_CPU, glu_op=O.GLU_SWIGLU, **kw)
+    want, want_sh = res if ts else (res, None)
+    assert O.rel_l2(got[ok], want[ok]) <= 1e-5
+    if bad_id:
+        assert bool((dst[-1, 2] == SENTINEL).all())
+    if ts:
+        assert O.rel_l2(sh.cpu().numpy(), want_sh) <= 1e-5
+
+
+@pytest.mark.parametrize("wtype,sh_type,K,R,n_tok,U,residual,bad_id", [
+    ("Q2_K", "Q4_K", 768, 4096, 1, 8, True, False),
+    ("Q3_K", "Q6_K", 512, 512, 3, 4, True, True),
+    ("Q5_K", None, 768, 1280, 2, 6, False, False),
+])
+def test_down_combine_q8K(torch_gpu, mc, O, wtype, sh_type, K, R, n_tok, U, residual, bad_id):
+    """fp32 rows quantized to q8_K in the launch: bit-identical to q8_K quantizer + q8_K GEMV +
+    combine, and within fp32 summation order of the oracle."""
+    torch = torch_gpu
+    md = import_module("a6000_custom_kernels_amd.moe_decode")
+    _note(f"down_combine q8_K {wtype}/{sh_type} K={K} R={R} tok={n_tok} U={U} res={residual} bad_id={bad_id}")
+    E = 16
+    tw = getattr(mc, wtype)
+    ts = getattr(mc, sh_type) if sh_type else None
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(K + R + U + 3)
+    down = md.random_expert_tensor(torch, tw, E, R, K, gen)
+    sh_down = md.random_expert_tensor(torch, ts, 1, R, K, gen)[0] if ts else None
+    rng = np.random.default_rng(R + n_tok + 1)
+    h = torch.from_numpy(rng.standard_normal((n_tok, U, K)).astype(np.float32)).cuda()
+    hs = torch.from_numpy(rng.standard_normal((n_tok, K)).astype(np.float32)).cuda()
+    x = torch.from_numpy(rng.standard_normal((n_tok, R)).astype(np.float32)).cuda() if residual else None
+    w = torch.from_numpy(rng.dirichlet(np.ones(U), n_tok).astype(np.float32)).cuda()
+    ids_np = np.stack([rng.choice(E, U, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    if bad_id:
+        ids_np[0, U - 1] = -2
+    ids = torch.from_numpy(ids_np).cuda()
+
+    # op by op: q8_K quantizer, q8_K GEMV, combine
+    hq = mc.quantize_q8_K(h.view(n_tok * U, K)).view(n_tok, U, -1)
+    hsq = mc.quantize_q8_K(hs)
+    o = torch.zeros((n_tok, U, R), dtype=torch.float32, device="cuda")
+    o_sh = torch.zeros((n_tok, R), dtype=torch.float32, device="cuda")
+    f_ref = mc.make_fusion(shared_up=sh_down, shared_dst=o_sh if ts else None, shared_type=ts if ts else -1,
+                           shared_src1=hsq if ts else None, shared_stride_col_y=K // 256)
+    mc.mul_mat_vec(wtype=tw, weights=down, ids=ids, y=hq, dst=o, K=K, R=R, n_experts=E, act=mc.ACT_Q8_K,
+                   fusion=f_ref, nchannels_y=U)
+    x_ref = torch.full((n_tok, R), SENTINEL, dtype=torch.float32, device="cuda")
+    mc.combine_q8_1(o, w, shared=o_sh if ts else None, residual=x, x_out=x_ref)
+
+    x_out = torch.full((n_tok, R), SENTINEL, dtype=torch.float32, device="cuda")
+    f = mc.make_fusion(shared_up=sh_down, shared_type=ts if ts else -1, shared_src1=hs if ts else None,
+                       shared_stride_col_y=K)
+    mc.ffn_down_combine(wtype=tw, weights=down, ids=ids, h=h, router_w=w, x_out=x_out, K=K, R=R, n_experts=E,
+                        residual=x, act=mc.ACT_F32 | mc.ACT_DOT_Q8_K, fusion=f)
+    torch.cuda.synchronize()
+    assert torch.equal(x_out, x_ref)
+    # the oracle on the same q8_K bytes
+    hq_np = hq.cpu().numpy()
+    assert np.array_equal(hq_np.reshape(n_tok * U, -1), np.stack([O.quantize_q8_K(r) for r in h.cpu().numpy().reshape(-1, K)]))
+    ok = (ids_np >= 0) & (ids_np < E)
+    kw = dict(sh_type=ts, sh_up=sh_down.cpu().numpy(), sh_act=hsq.cpu().numpy()) if ts else {}
+    res = O.mul_mat_id(wtype=tw, K=K, R=R, n_as=E, src0=down.cpu().numpy(), ids=np.where(ok, ids_np, 0).astype(np.int32),
+                       act=hq_np, act_kind=O.ACT_CPU, nchannels_y=U, **kw)
+    want_o, want_sh = res if ts else (res, None)
+    want_o = np.where(ok[:, :, None], want_o, 0.0).astype(np.float32)
+    want_x, _ = O.combine_q8_1(want_o, w.cpu().numpy(), shared=want_sh, residual=x.cpu().numpy() if residual else None)
+    assert O.rel_l2(x_out.cpu().numpy(), want_x) <= 1e-5
+
+
+def test_fused_q8K_decode_against_ggml_cpu(torch_gpu, mc, O):
+    """The headline decode block in q8_K mode against the ggml-CPU MUL_MAT_ID restatement
+    (fp32 src1 quantized to q8_K inside, K-quant x q8_K dots), op by op: RMSNorm, gate/up +
+    SwiGLU, down, router-weighted combine with the shared expert and the residual."""
+    torch = torch_gpu
+    md = import_module("a6000_custom_kernels_amd.moe_decode")
+    m = md.MoeDecodeModel(torch, n_layers=2, n_experts=32, hidden=2048, ffn=768, n_used=8, seed=12, act="q8_K")
+    H, F, U, E = m.H, m.F, m.U, m.E
+    ids, w = md.make_routing(1, m.L, E, U, seed=4)
+    x0 = (np.random.default_rng(13).standard_normal((1, H)) * 2).astype(np.float32)
+    m.x.copy_(torch.from_numpy(x0))
+    m.set_routing(torch.from_numpy(ids[0]), torch.from_numpy(w[0]))
+    m.launch_token()
+    torch.cuda.synchronize()
+    got = m.x.cpu().numpy()
+    x = x0.copy()
+    for l in range(m.L):
+        ly = m.layers[l]
+        lid = ids[0, l].reshape(1, U)
+        y = _normalized(O, x, m.norm[l].cpu().numpy(), m.eps).reshape(1, 1, H)
+        cpu = lambda wt, t, K, R, n_as, src1, i: O.cpu_mul_mat_id_f32(wtype=wt, K=K, R=R, n_as=n_as,  # noqa: E731
+                                                                      src0=t.cpu().numpy().reshape(n_as, R, -1),
+                                                                      src1=src1, ids=i)
+        g = cpu(m.wtype, ly.gate, H, F, E, y, lid)
+        u = cpu(m.wtype, ly.up, H, F, E, y, lid)
+        z = np.zeros((1, 1), np.int32)
+        sg = cpu(m.sh_type, ly.sh_gate, H, F, 1, y, z)
+        su = cpu(m.sh_type, ly.sh_up, H, F, 1, y, z)
+        glu = np.vectorize(lambda a, b: O.glu(O.GLU_SWIGLU, float(a), float(b), 0.0), otypes=[np.float32])
+        hh = glu(g, u).reshape(1, U, F)
+        hs = glu(sg, su).reshape(1, 1, F)
+        o = cpu(m.wtype, ly.down, F, H, E, hh, lid)
+        osh = cpu(m.sh_type, ly.sh_down, F, H, 1, hs, z).reshape(1, H)
+        x, _ = O.combine_q8_1(o.reshape(1, U, H), w[0, l].reshape(1, U), shared=osh, residual=x)
+    err = O.rel_l2(got, x)
+    _note(f"  q8_K decode vs ggml-CPU rel_l2={err:.3e}")
+    assert err <= 1e-3
