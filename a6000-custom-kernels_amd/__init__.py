@@ -67,7 +67,8 @@ class Node(C.Structure):
 
 class Config(C.Structure):
     _fields_ = [("enabled", C.c_int32), ("slots", C.c_int32), ("budget_gb", C.c_double), ("margin_gb", C.c_double),
-                ("seed_path", C.c_char_p), ("max_promotions", C.c_int32), ("verbose", C.c_int32)]
+                ("seed_path", C.c_char_p), ("max_promotions", C.c_int32), ("verbose", C.c_int32),
+                ("async_promotions", C.c_int32)]
 
 
 class EntryInfo(C.Structure):
@@ -467,12 +468,13 @@ def ssm_conv(x, w, *, bias=None, silu=False, out=None, n_t=None, stream=None):
 
 
 def configure(*, enabled=True, slots=-1, budget_gb=0.0, margin_gb=2.0, seed_path=None, max_promotions=48,
-              verbose=False):
+              verbose=False, async_promotions=False):
     cfg = Config()
     cfg.enabled, cfg.slots, cfg.budget_gb, cfg.margin_gb = int(enabled), slots, budget_gb, margin_gb
     cfg._seed = seed_path.encode() if seed_path else None
     cfg.seed_path = cfg._seed
     cfg.max_promotions, cfg.verbose = max_promotions, int(verbose)
+    cfg.async_promotions = int(async_promotions)
     check(lib().ggml_hip_moe_cache_configure(C.byref(cfg)), "configure")
 
 

@@ -27,6 +27,14 @@ struct Device {
     virtual int copy_d2h(void *dst, const void *src, size_t n, void *stream) = 0;   // async on stream
     virtual int memset_dev(void *dst, int v, size_t n, void *stream) = 0;           // async on stream
     virtual int sync(void *stream) = 0;
+    // a second stream (default priority) and events ordering it against the caller's stream
+    virtual int stream_create(void **stream) = 0;
+    virtual int stream_destroy(void *stream) = 0;
+    virtual int event_create(void **event) = 0;
+    virtual int event_destroy(void *event) = 0;
+    virtual int event_record(void *event, void *stream) = 0;
+    virtual int stream_wait_event(void *stream, void *event) = 0;
+    virtual int event_sync(void *event) = 0;
     virtual int mem_info(size_t *free_b, size_t *total_b) = 0;
     virtual int ptr_kind(const void *p) = 0;                               // PtrKind
     virtual int host_device_ptr(const void *host, void **dev) = 0;         // device-visible address of host memory

@@ -31,6 +31,15 @@ struct HipDevice final : Device {
         return (int) hipMemsetAsync(dst, v, n, (hipStream_t) s);
     }
     int sync(void *s) override { return (int) hipStreamSynchronize((hipStream_t) s); }
+    int stream_create(void **s) override {
+        return (int) hipStreamCreateWithFlags((hipStream_t *) s, hipStreamNonBlocking);   // default priority
+    }
+    int stream_destroy(void *s) override { return (int) hipStreamDestroy((hipStream_t) s); }
+    int event_create(void **e) override { return (int) hipEventCreateWithFlags((hipEvent_t *) e, hipEventDisableTiming); }
+    int event_destroy(void *e) override { return (int) hipEventDestroy((hipEvent_t) e); }
+    int event_record(void *e, void *s) override { return (int) hipEventRecord((hipEvent_t) e, (hipStream_t) s); }
+    int stream_wait_event(void *s, void *e) override { return (int) hipStreamWaitEvent((hipStream_t) s, (hipEvent_t) e, 0); }
+    int event_sync(void *e) override { return (int) hipEventSynchronize((hipEvent_t) e); }
     int mem_info(size_t *f, size_t *t) override { return (int) hipMemGetInfo(f, t); }
     int ptr_kind(const void *p) override {
         hipPointerAttribute_t attr;

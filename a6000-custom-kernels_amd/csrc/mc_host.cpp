@@ -63,6 +63,7 @@ struct Config {
     bool verbose = false;
     bool debug = false;
     bool allow_register = false;
+    bool async_promotions = false;        // promotion copies on a second stream (see step_locked)
 };
 
 Config g_cfg;
@@ -91,6 +92,8 @@ void read_env_locked() {
     c.verbose = c.debug || getenv("GGML_HIP_MOE_CACHE_VERBOSE") != nullptr;
     const char *ar = getenv("GGML_HIP_MOE_CACHE_ALLOW_REGISTER");
     c.allow_register = ar && ar[0] == '1';
+    const char *as = getenv("GGML_HIP_MOE_CACHE_ASYNC");
+    c.async_promotions = as && as[0] == '1';
     g_cfg = c;
     g_cfg_ready = true;
     if (g_cfg.enabled && g_cfg.verbose) {
@@ -114,12 +117,16 @@ struct Entry {
     char *pool = nullptr;                // device, n_slots * expert_bytes
     uint64_t *d_tbl = nullptr;           // device, tagged pointers
     std::vector<uint64_t> h_tbl;         // host mirror
-    uint32_t *d_stamps = nullptr;        // device, last-use clock per expert
+    uint32_t *d_stamps = nullptr;        // device, last-use clock per expert (a slice of the stamps arena,
+                                         // or its own allocation when the arena is full)
+    bool stamps_in_arena = false;
+    size_t stamps_off = 0;               // word offset of the slice in the arena
     std::vector<int32_t> slot_of;        // expert -> slot (-1: cold)
     std::vector<int32_t> expert_of;      // slot -> expert (-1: free)
     std::vector<uint32_t> h_stamps;      // host mirror of d_stamps for eviction
     uint32_t stamps_clock = 0;           // clock at the last mirror refresh
     bool tbl_dirty = false;
+    uint64_t *h_tbl_stage[2] = {nullptr, nullptr};   // pinned table snapshots (asynchronous promotions)
     std::string name;
 };
 
@@ -140,11 +147,24 @@ uint32_t *g_d_stats = nullptr;                       // device [STATS_WORDS]
 uint32_t *g_h_stats = nullptr;                       // pinned host mirror (+1 word: clock staging)
 uint32_t *g_d_clock = nullptr;
 uint32_t g_h_clock = 0;
+// every tensor's eviction stamps in one device array (and its pinned mirror), so a step reads
+// the stamps it needs with one copy
+constexpr size_t STAMPS_ARENA_WORDS = size_t(1) << 20;
+uint32_t *g_d_stamps_arena = nullptr;
+uint32_t *g_h_stamps_arena = nullptr;
+size_t g_stamps_used = 0;                            // words handed out
 size_t g_used = 0;                                   // pool bytes allocated
 std::unordered_map<uint32_t, int> g_admission;       // (id << 12 | expert) -> sightings
 std::unordered_map<std::string, std::vector<int>> g_seed;
 bool g_seed_loaded = false;
 ggml_hip_moe_totals g_totals = {};
+
+// asynchronous promotions: the copy stream, the event ordering it after the compute stream's
+// demotions, and the event of its last table flush (waited for before the next step)
+void *g_copy_stream = nullptr;
+void *g_order_event = nullptr;
+void *g_copy_event = nullptr;
+bool g_copy_pending = false;
 
 std::unordered_map<const void *, int> g_ptr_kind;    // cached residency test
 std::mutex g_ptr_mutex;
@@ -178,6 +198,10 @@ int init_globals_locked(void *stream) {
     if ((rc = dev()->malloc_dev((void **) &g_d_stats, sizeof(uint32_t) * STATS_WORDS))) return dev_err(rc, "stats alloc");
     if ((rc = dev()->malloc_host((void **) &g_h_stats, sizeof(uint32_t) * (STATS_WORDS + 2)))) return dev_err(rc, "pinned stats alloc");
     if ((rc = dev()->malloc_dev((void **) &g_d_clock, sizeof(uint32_t)))) return dev_err(rc, "clock alloc");
+    if ((rc = dev()->malloc_dev((void **) &g_d_stamps_arena, sizeof(uint32_t) * STAMPS_ARENA_WORDS))) return dev_err(rc, "stamps arena alloc");
+    if ((rc = dev()->malloc_host((void **) &g_h_stamps_arena, sizeof(uint32_t) * STAMPS_ARENA_WORDS)))
+        return dev_err(rc, "pinned stamps arena alloc");
+    g_stamps_used = 0;
     memset(g_h_stats, 0, sizeof(uint32_t) * (STATS_WORDS + 2));
     if ((rc = dev()->memset_dev(g_d_stats, 0, sizeof(uint32_t) * STATS_WORDS, stream))) return dev_err(rc, "stats clear");
     if ((rc = dev()->memset_dev(g_d_clock, 0, sizeof(uint32_t), stream))) return dev_err(rc, "clock clear");
@@ -264,7 +288,7 @@ int get_or_create_locked(const ggml_hip_moe_tensor *src0, void *stream, Entry **
     // a later call never finds an entry whose device table was not written.
     auto abandon = [&](int code, const char *what) {
         if (e->pool) dev()->free_dev(e->pool);
-        if (e->d_stamps) dev()->free_dev(e->d_stamps);
+        if (e->d_stamps && !e->stamps_in_arena) dev()->free_dev(e->d_stamps);
         if (e->d_tbl) dev()->free_dev(e->d_tbl);
         delete e;
         return dev_err(code, what);
@@ -272,7 +296,15 @@ int get_or_create_locked(const ggml_hip_moe_tensor *src0, void *stream, Entry **
     e->h_tbl.resize(e->n_experts);
     for (int i = 0; i < e->n_experts; ++i) e->h_tbl[i] = host_entry(e, i);
     if ((rc = dev()->malloc_dev((void **) &e->d_tbl, sizeof(uint64_t) * e->n_experts))) return abandon(rc, "table alloc");
-    if ((rc = dev()->malloc_dev((void **) &e->d_stamps, sizeof(uint32_t) * e->n_experts))) return abandon(rc, "stamps alloc");
+    const size_t sw = ((size_t) e->n_experts + 63) & ~(size_t) 63;      // 256-byte slices
+    if (g_d_stamps_arena && g_stamps_used + sw <= STAMPS_ARENA_WORDS) {
+        e->d_stamps = g_d_stamps_arena + g_stamps_used;
+        e->stamps_in_arena = true;
+        e->stamps_off = g_stamps_used;
+        g_stamps_used += sw;                       // (an abandoned registration leaves its slice unused)
+    } else if ((rc = dev()->malloc_dev((void **) &e->d_stamps, sizeof(uint32_t) * e->n_experts))) {
+        return abandon(rc, "stamps alloc");
+    }
     if ((rc = dev()->memset_dev(e->d_stamps, 0, sizeof(uint32_t) * e->n_experts, stream))) return abandon(rc, "stamps clear");
     e->h_stamps.assign(e->n_experts, 0);
     e->slot_of.assign(e->n_experts, -1);
@@ -352,8 +384,47 @@ int acquire_slot_locked(Entry *e, void *stream, int *slot_out) {
 }
 
 // between-graph promotion step (kernels/moe-cache.cu:669-775)
+// Waits for the previous step's asynchronous promotions (copy stream) to finish.
+int wait_copies_locked() {
+    if (!g_copy_pending) return 0;
+    int rc;
+    if ((rc = dev()->event_sync(g_copy_event))) return dev_err(rc, "promotion copies");
+    g_copy_pending = false;
+    return 0;
+}
+
+// Uploads entry e's host table through its pinned snapshot `which` on `stream` (the
+// snapshot keeps the bytes of this upload while the host table changes).
+int upload_table_staged_locked(Entry *e, int which, void *stream) {
+    int rc;
+    if (!e->h_tbl_stage[which]) {
+        void *p = nullptr;
+        if ((rc = dev()->malloc_host(&p, sizeof(uint64_t) * e->n_experts))) return dev_err(rc, "table staging");
+        e->h_tbl_stage[which] = (uint64_t *) p;
+    }
+    memcpy(e->h_tbl_stage[which], e->h_tbl.data(), sizeof(uint64_t) * e->n_experts);
+    if ((rc = dev()->copy_h2d(e->d_tbl, e->h_tbl_stage[which], sizeof(uint64_t) * e->n_experts, stream)))
+        return dev_err(rc, "table flush");
+    return 0;
+}
+
+// The step between tokens (kernels/moe-cache.cu:742-775): stats readback, clock, admission on
+// the second sighting, LRU promotion, one table upload per touched tensor.
+//
+// The eviction stamps of every tensor the miss log could make evict are read back in one
+// batch with one wait, so the loop below never waits on the stream (its lazy readback in
+// acquire_slot_locked finds them fresh); the decisions are those of reading them lazily.
+//
+// With async_promotions the promotion copies leave the caller's stream: the demotions
+// (victims back to their host entries) are uploaded on it first, so the next token's
+// kernels never read a slot that is being overwritten; the copies and then the promoted
+// entries' table upload go on a second stream ordered after that upload.  A kernel running
+// meanwhile reads each table entry either before or after its 8-byte update, and both point
+// at the expert's bytes, so results are unchanged; which reads hit the pool (the hit / miss
+// counts and stamps) then depends on timing.
 int step_locked(void *stream) {
     int rc;
+    if ((rc = wait_copies_locked())) return rc;
     if ((rc = dev()->copy_d2h(g_h_stats, g_d_stats, sizeof(uint32_t) * STATS_WORDS, stream))) return dev_err(rc, "stats readback");
     if ((rc = dev()->sync(stream))) return dev_err(rc, "stream sync");
     uint32_t n = g_h_stats[0];
@@ -381,7 +452,52 @@ int step_locked(void *stream) {
     }
     if (n == 0) return 0;
 
+    // stamps of the tensors that may evict: more possible promotions (second sightings, counted on
+    // a copy of the admission counts) than free slots; the arena's used prefix comes back in one copy
+    {
+        std::unordered_map<uint32_t, int> counts;
+        std::unordered_map<Entry *, uint32_t> possible;
+        for (uint32_t i = 0; i < n; ++i) {
+            const uint32_t packed = g_h_stats[LOG_BASE + i];
+            const int32_t cid = (int32_t) (packed >> 12);
+            auto it = counts.find(packed);
+            if (it == counts.end()) {
+                auto ga = g_admission.find(packed);
+                it = counts.emplace(packed, ga == g_admission.end() ? 0 : ga->second).first;
+            }
+            if (++it->second < 2) continue;
+            it->second = 0;
+            if (cid >= 0 && cid < (int32_t) g_all.size()) possible[g_all[cid]] += 1;
+        }
+        std::vector<Entry *> need;
+        bool arena = false;
+        for (auto &kv : possible) {
+            Entry *e = kv.first;
+            if (e->n_slots == 0 || e->stamps_clock == g_h_clock) continue;
+            uint32_t free_slots = 0;
+            for (int sl = 0; sl < e->n_slots; ++sl) free_slots += e->expert_of[sl] < 0 ? 1 : 0;
+            if (free_slots >= kv.second) continue;
+            need.push_back(e);
+            if (e->stamps_in_arena) {
+                arena = true;
+            } else if ((rc = dev()->copy_d2h(e->h_stamps.data(), e->d_stamps, sizeof(uint32_t) * e->n_experts, stream))) {
+                return dev_err(rc, "stamps readback");
+            }
+        }
+        if (arena && (rc = dev()->copy_d2h(g_h_stamps_arena, g_d_stamps_arena, sizeof(uint32_t) * g_stamps_used, stream)))
+            return dev_err(rc, "stamps readback");
+        if (!need.empty() && (rc = dev()->sync(stream))) return dev_err(rc, "stream sync");
+        for (Entry *e : need) {
+            if (e->stamps_in_arena)
+                memcpy(e->h_stamps.data(), g_h_stamps_arena + e->stamps_off, sizeof(uint32_t) * e->n_experts);
+            e->stamps_clock = g_h_clock;
+        }
+    }
+
     // admission: promote on the 2nd sighting; the count resets even when promotion fails
+    struct Promo { Entry *e; int slot, expert; };
+    std::vector<Promo> deferred;                     // asynchronous promotions
+    const bool async = g_cfg.async_promotions;
     int promoted = 0;
     for (uint32_t i = 0; i < n && promoted < g_cfg.max_promotions; ++i) {
         const uint32_t packed = g_h_stats[LOG_BASE + i];
@@ -397,21 +513,58 @@ int step_locked(void *stream) {
         int slot;
         if ((rc = acquire_slot_locked(e, stream, &slot))) return rc;
         if (slot < 0) continue;
-        if ((rc = dev()->copy_h2d(e->pool + (size_t) slot * e->expert_bytes, e->data + (size_t) expert * e->expert_bytes,
-                                  e->expert_bytes, stream)))
-            return dev_err(rc, "promotion copy");
-        e->h_tbl[expert] = pool_entry(e, slot);
-        e->tbl_dirty = true;
+        if (async) {
+            deferred.push_back(Promo{e, slot, expert});
+        } else {
+            if ((rc = dev()->copy_h2d(e->pool + (size_t) slot * e->expert_bytes, e->data + (size_t) expert * e->expert_bytes,
+                                      e->expert_bytes, stream)))
+                return dev_err(rc, "promotion copy");
+            e->h_tbl[expert] = pool_entry(e, slot);
+            e->tbl_dirty = true;
+        }
         e->slot_of[expert] = slot;
         e->expert_of[slot] = expert;
         promoted += 1;
         g_totals.promotions += 1;
     }
-    // one table upload per touched tensor, after the pool copies
-    for (Entry *e : g_all) {
-        if (!e->tbl_dirty) continue;
-        if ((rc = dev()->copy_h2d(e->d_tbl, e->h_tbl.data(), sizeof(uint64_t) * e->n_experts, stream))) return dev_err(rc, "table flush");
-        e->tbl_dirty = false;
+    if (!async) {
+        // one table upload per touched tensor, after the pool copies
+        for (Entry *e : g_all) {
+            if (!e->tbl_dirty) continue;
+            if ((rc = dev()->copy_h2d(e->d_tbl, e->h_tbl.data(), sizeof(uint64_t) * e->n_experts, stream))) return dev_err(rc, "table flush");
+            e->tbl_dirty = false;
+        }
+    } else {
+        // demotions on the caller's stream, ahead of the next token's kernels
+        for (Entry *e : g_all) {
+            if (!e->tbl_dirty) continue;
+            if ((rc = upload_table_staged_locked(e, 0, stream))) return rc;
+            e->tbl_dirty = false;
+        }
+        if (!deferred.empty()) {
+            if (!g_copy_stream && (rc = dev()->stream_create(&g_copy_stream))) return dev_err(rc, "copy stream");
+            if (!g_order_event && (rc = dev()->event_create(&g_order_event))) return dev_err(rc, "event");
+            if (!g_copy_event && (rc = dev()->event_create(&g_copy_event))) return dev_err(rc, "event");
+            if ((rc = dev()->event_record(g_order_event, stream))) return dev_err(rc, "event record");
+            if ((rc = dev()->stream_wait_event(g_copy_stream, g_order_event))) return dev_err(rc, "stream wait");
+            // a slot taken twice this step (its first promotion evicted again) keeps its last expert
+            for (const Promo &p : deferred) {
+                if (p.e->expert_of[p.slot] != p.expert) continue;
+                if ((rc = dev()->copy_h2d(p.e->pool + (size_t) p.slot * p.e->expert_bytes,
+                                          p.e->data + (size_t) p.expert * p.e->expert_bytes, p.e->expert_bytes,
+                                          g_copy_stream)))
+                    return dev_err(rc, "promotion copy");
+                p.e->h_tbl[p.expert] = pool_entry(p.e, p.slot);
+                p.e->tbl_dirty = true;
+            }
+            for (Entry *e : g_all) {
+                if (!e->tbl_dirty) continue;
+                if ((rc = upload_table_staged_locked(e, 1, g_copy_stream))) return rc;
+                e->tbl_dirty = false;
+            }
+            if ((rc = dev()->event_record(g_copy_event, g_copy_stream))) return dev_err(rc, "event record");
+            g_copy_pending = true;
+        }
     }
     if (g_admission.size() > 8192) {
         for (auto it = g_admission.begin(); it != g_admission.end();) {
@@ -1285,6 +1438,7 @@ int ggml_hip_moe_cache_configure(const ggml_hip_moe_config *cfg) {
     c.verbose = cfg->verbose != 0;
     c.debug = false;
     c.allow_register = g_cfg.allow_register;
+    c.async_promotions = cfg->async_promotions != 0;
     g_cfg = c;
     g_cfg_ready = true;
     g_seed.clear();
@@ -1303,6 +1457,7 @@ int ggml_hip_moe_cache_get_config(ggml_hip_moe_config *out) {
     out->seed_path = g_cfg.seed_path.c_str();
     out->max_promotions = g_cfg.max_promotions;
     out->verbose = g_cfg.verbose;
+    out->async_promotions = g_cfg.async_promotions ? 1 : 0;
     return 0;
 }
 
@@ -1413,10 +1568,19 @@ int ggml_hip_moe_cache_reset(void) {
     std::lock_guard<std::mutex> lock(g_mutex);
     int first_rc = 0;
     auto note = [&](int rc) { if (rc && !first_rc) first_rc = rc; };
+    // pending promotion copies write into the pools freed below
+    if (g_copy_pending) note(dev()->event_sync(g_copy_event));
+    g_copy_pending = false;
+    if (g_copy_event) note(dev()->event_destroy(g_copy_event));
+    if (g_order_event) note(dev()->event_destroy(g_order_event));
+    if (g_copy_stream) note(dev()->stream_destroy(g_copy_stream));
+    g_copy_event = g_order_event = g_copy_stream = nullptr;
     for (Entry *e : g_all) {
+        for (uint64_t *&st : e->h_tbl_stage)
+            if (st) note(dev()->free_host(st));
         if (e->pool) note(dev()->free_dev(e->pool));
         if (e->d_tbl) note(dev()->free_dev(e->d_tbl));
-        if (e->d_stamps) note(dev()->free_dev(e->d_stamps));
+        if (e->d_stamps && !e->stamps_in_arena) note(dev()->free_dev(e->d_stamps));
         delete e;
     }
     g_all.clear();
@@ -1429,7 +1593,10 @@ int ggml_hip_moe_cache_reset(void) {
     if (g_d_stats) note(dev()->free_dev(g_d_stats));
     if (g_d_clock) note(dev()->free_dev(g_d_clock));
     if (g_h_stats) note(dev()->free_host(g_h_stats));
-    g_d_stats = g_d_clock = g_h_stats = nullptr;
+    if (g_d_stamps_arena) note(dev()->free_dev(g_d_stamps_arena));
+    if (g_h_stamps_arena) note(dev()->free_host(g_h_stamps_arena));
+    g_d_stats = g_d_clock = g_h_stats = g_d_stamps_arena = g_h_stamps_arena = nullptr;
+    g_stamps_used = 0;
     g_h_clock = 0;
     g_used = 0;
     g_admission.clear();

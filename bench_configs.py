@@ -337,11 +337,11 @@ def cfg3(torch, mc, md, rounds, tokens=256, calib_tokens=32, layers=40):
                 1, mc.ACT_F32, C.byref(tens[(l, "down")]), None, None, h.data_ptr(), ids_dev[l].data_ptr(),
                 o.data_ptr(), F, H, E, 1, U, U, U * F, U * H, F, H, U, sp), "down")
 
-    def run(tag, slots, n_top, n_tok, max_promotions):
+    def run(tag, slots, n_top, n_tok, max_promotions, async_promotions=False):
         mc.reset()
         path = seed_file(f"/tmp/moe_seed_{tag}.txt", n_top) if n_top else None
         mc.configure(enabled=True, slots=slots, budget_gb=0.0, margin_gb=2.0, seed_path=path,
-                     max_promotions=max_promotions)
+                     max_promotions=max_promotions, async_promotions=async_promotions)
         ids = route(n_tok + 1)
         ids_t = torch.from_numpy(ids).cuda()
         with torch.cuda.stream(s):
@@ -399,6 +399,12 @@ def cfg3(torch, mc, md, rounds, tokens=256, calib_tokens=32, layers=40):
           "PCIe_GB/s_misses": round(miss_bytes / t_miss / 1e9, 2) if miss_bytes else None,
           "tok_per_s_gpu": round(1e6 / mix["us_per_token_gpu"], 1),
           "tok_per_s_with_step": round(1e6 / mix["us_per_token_wall"], 1)})
+    # the same run with the promotion copies on the library's second stream
+    mixa = run("mixed_async", POOL, POOL, tokens, 48, async_promotions=True)
+    emit({"config": "cfg3", "run": f"{layers} layers, as above, promotion copies on a second stream "
+                                   "(async_promotions)", **mixa, "layers": layers,
+          "tok_per_s_gpu": round(1e6 / mixa["us_per_token_gpu"], 1),
+          "tok_per_s_with_step": round(1e6 / mixa["us_per_token_wall"], 1)})
     mc.reset()
 
 

@@ -340,6 +340,11 @@ typedef struct ggml_hip_moe_config {
     const char *seed_path;      /* seed file; NULL or "": none */
     int32_t     max_promotions; /* per step (reference: 48) */
     int32_t     verbose;        /* registration / step lines on stderr */
+    int32_t     async_promotions; /* 1: ggml_hip_moe_cache_step issues the promotion copies on a
+                                   * second stream of its own (env GGML_HIP_MOE_CACHE_ASYNC=1): the
+                                   * next token no longer waits for them, results are unchanged,
+                                   * and which of its reads hit the pool depends on timing.
+                                   * 0 (default): the reference's order on the caller's stream. */
 } ggml_hip_moe_config;
 
 /* Replaces the env-derived settings; must be called before the first registration. */

@@ -70,7 +70,7 @@ GATE_MODES = ("cache", "device", "device_host_desc", "none")
 
 def run_scenario(mc_mod, lib, backend, *, n_experts=16, R=40, K=4096, wtype=10, slots=5, steps=12, n_tok=2,
                  n_used=4, seed_path=None, free_bytes, max_promotions=48, check_outputs=None, rng_seed=1234,
-                 gate_mode="cache", shared_bias=False):
+                 gate_mode="cache", shared_bias=False, async_promotions=False, after_step=None):
     """backend: object with
          host_tensor(nbytes, role) -> (ptr, keepalive)  GPU-readable host memory holding the weights of `role`
          device_tensor(nbytes, role) -> (ptr, keepalive) device memory holding the weights of `role`
@@ -85,7 +85,10 @@ def run_scenario(mc_mod, lib, backend, *, n_experts=16, R=40, K=4096, wtype=10, 
                            wants() refuses;
                   "none"   no gate.
        Only a cache-managed gate is recorded (kernels/moe-cache.cu:178-201, :804): the model sees gate=None
-       otherwise.  check_outputs(step, ids) is called after each GEMV when given (GPU backend)."""
+       otherwise.  check_outputs(step, ids) is called after each GEMV when given (GPU backend).
+       async_promotions: the step's promotion copies go on the library's second stream; after_step()
+       (e.g. a device-wide synchronize) runs after each step, before the state is compared, so the
+       next GEMV sees every promotion, as the model assumes."""
     assert gate_mode in GATE_MODES, gate_mode
     rng = np.random.default_rng(rng_seed)
     cfg = mc_mod.Config()
@@ -93,6 +96,7 @@ def run_scenario(mc_mod, lib, backend, *, n_experts=16, R=40, K=4096, wtype=10, 
     sp = seed_path.encode() if seed_path else None
     cfg.seed_path = sp
     cfg.max_promotions, cfg.verbose = max_promotions, 0
+    cfg.async_promotions = int(async_promotions)
     assert lib.ggml_hip_moe_cache_reset() == 0
     assert lib.ggml_hip_moe_cache_configure(C.byref(cfg)) == 0, lib.ggml_hip_moe_last_error()
 
@@ -146,6 +150,8 @@ def run_scenario(mc_mod, lib, backend, *, n_experts=16, R=40, K=4096, wtype=10, 
         if check_outputs is not None:
             check_outputs(step, ids)
         assert lib.ggml_hip_moe_cache_step(stream) == 0, lib.ggml_hip_moe_last_error()
+        if after_step is not None:
+            after_step()
         model.step()
         compare_state(mc_mod, lib, model, f"step {step} after promotion")
         tot = mc_mod.Totals()

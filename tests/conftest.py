@@ -73,4 +73,5 @@ def sim(mc):
     lib.mc_sim_fail_h2d_after.argtypes = [C.c_int]
     lib.mc_sim_live_regions.restype = C.c_longlong
     lib.mc_sim_counters.argtypes = [C.c_void_p]
+    lib.mc_sim_live_streams_events.argtypes = [C.c_void_p]
     return lib

@@ -76,6 +76,38 @@ struct SimDevice final : Device {
         n_sync++;
         return 0;
     }
+    // every simulated copy completes when issued: streams and events only keep count
+    long long live_streams = 0, live_events = 0, n_event_sync = 0;
+    int stream_create(void **s) override {
+        std::lock_guard<std::mutex> l(m);
+        *s = new char(0);
+        live_streams++;
+        return 0;
+    }
+    int stream_destroy(void *s) override {
+        std::lock_guard<std::mutex> l(m);
+        delete (char *) s;
+        live_streams--;
+        return 0;
+    }
+    int event_create(void **e) override {
+        std::lock_guard<std::mutex> l(m);
+        *e = new char(0);
+        live_events++;
+        return 0;
+    }
+    int event_destroy(void *e) override {
+        std::lock_guard<std::mutex> l(m);
+        delete (char *) e;
+        live_events--;
+        return 0;
+    }
+    int event_record(void *, void *) override { return 0; }
+    int stream_wait_event(void *, void *) override { return 0; }
+    int event_sync(void *) override {
+        n_event_sync++;
+        return 0;
+    }
     int mem_info(size_t *f, size_t *t) override {
         *f = free_b;
         *t = total_b;
@@ -192,6 +224,12 @@ long long mc_sim_alloc_count(void) { return mc::g_sim.n_alloc; }
 long long mc_sim_live_regions(void) {
     std::lock_guard<std::mutex> l(mc::g_sim.m);
     return (long long) mc::g_sim.regions.size();
+}
+
+// live streams and events of the simulated device
+void mc_sim_live_streams_events(long long *out2) {
+    out2[0] = mc::g_sim.live_streams;
+    out2[1] = mc::g_sim.live_events;
 }
 
 void mc_sim_counters(long long *out5) {

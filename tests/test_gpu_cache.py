@@ -125,6 +125,24 @@ def test_cache_scenario_gpu(torch_gpu, mc, O, tmp_path, wtype, slots, seeded):
     assert mc.lib().ggml_hip_moe_cache_reset() == 0
 
 
+@pytest.mark.parametrize("wtype,slots,n_tok", [(10, 5, 2), (12, 3, 3)])
+def test_cache_async_promotions_gpu(torch_gpu, mc, O, wtype, slots, n_tok):
+    """Promotion copies on the library's second stream: outputs against the resident path and the
+    oracle every step; with a device-wide synchronize after each step (so the next GEMV sees every
+    promotion) the recorder and LRU state follow the cache model exactly."""
+    torch = torch_gpu
+    print(f"cache async promotions type={wtype} slots={slots} n_tok={n_tok}", flush=True)
+    n_experts, R, K = 16, 64, 4096
+    be = GpuBackend(torch, mc, O, n_experts, R, K, wtype, seed=970 + wtype)
+    free_b = torch.cuda.mem_get_info()[0]
+    model, keep = S.run_scenario(mc, mc.lib(), be, n_experts=n_experts, R=R, K=K, wtype=wtype, slots=slots, steps=10,
+                                 n_tok=n_tok, n_used=4, free_bytes=free_b, check_outputs=be.check_outputs,
+                                 rng_seed=23 + n_tok, async_promotions=True, after_step=torch.cuda.synchronize)
+    assert model.promotions > 0 and model.evictions > 0
+    torch.cuda.synchronize()
+    assert mc.lib().ggml_hip_moe_cache_reset() == 0
+
+
 @pytest.mark.parametrize("gate_mode,shared_bias", [("device", False), ("device_host_desc", False), ("none", False),
                                                     ("cache", True), ("device", True)])
 def test_cache_gate_modes_gpu(torch_gpu, mc, O, gate_mode, shared_bias):

@@ -81,6 +81,46 @@ def test_sim_gate_modes_match_model(sim, mc, gate_mode, shared_bias):
     assert model.promotions > 0 and model.evictions > 0
 
 
+@pytest.mark.parametrize("slots,n_tok,max_promo,rseed,gate_mode", [
+    (5, 2, 48, 21, "cache"), (3, 4, 2, 22, "cache"), (1, 3, 5, 23, "device")])
+def test_sim_async_promotions_match_model(sim, mc, slots, n_tok, max_promo, rseed, gate_mode):
+    """Promotion copies on the second stream: the simulated device completes every copy when it is
+    issued, so the registry, tables, pools and counters must follow the model step for step; the
+    stream and events go away with reset."""
+    sim.mc_sim_set_mem_info(64 << 30, 64 << 30)
+    model, keep = S.run_scenario(mc, sim, SimBackend(sim), n_experts=16, R=8, K=256, wtype=10, slots=slots, steps=25,
+                                 n_tok=n_tok, n_used=4, free_bytes=64 << 30, max_promotions=max_promo, rng_seed=rseed,
+                                 gate_mode=gate_mode, async_promotions=True)
+    assert model.promotions > 0 and (slots >= 16 or model.evictions > 0)
+    se = (C.c_longlong * 2)()
+    sim.mc_sim_live_streams_events(se)
+    assert se[0] == 1 and se[1] == 2                 # one copy stream, its two events
+    assert sim.ggml_hip_moe_cache_reset() == 0
+    sim.mc_sim_live_streams_events(se)
+    assert se[0] == 0 and se[1] == 0
+
+
+def test_sim_step_reads_stamps_in_one_batch(sim, mc):
+    """A step that evicts in several tensors reads their stamps with one wait, not one per tensor."""
+    sim.mc_sim_set_mem_info(64 << 30, 64 << 30)
+    cnt = (C.c_longlong * 5)()
+    before, after = [], []
+
+    def pre(step, ids):                              # called right before each step
+        sim.mc_sim_counters(cnt)
+        before.append(cnt[3])
+
+    def post():
+        sim.mc_sim_counters(cnt)
+        after.append(cnt[3])
+    model, keep = S.run_scenario(mc, sim, SimBackend(sim), n_experts=16, R=8, K=256, wtype=10, slots=2, steps=12,
+                                 n_tok=3, n_used=4, free_bytes=64 << 30, rng_seed=31, gate_mode="cache",
+                                 check_outputs=pre, after_step=post)
+    # each step: the stats wait and at most one stamps wait, though both tensors (up, gate) evict
+    per_step = np.array(after) - np.array(before)
+    assert model.evictions > 4 and per_step.max() == 2, per_step
+
+
 @pytest.mark.parametrize("fail_after,what", [(4, b"table upload"), (2, b"seed copy")])
 def test_sim_failed_registration_leaves_nothing(sim, mc, tmp_path, fail_after, what):
     """A failing seed copy or table upload frees the pool, table and stamps and registers nothing, so a
@@ -104,7 +144,7 @@ def test_sim_failed_registration_leaves_nothing(sim, mc, tmp_path, fail_after, w
     set_ids(np.array([[0, 1]], np.int32))
     y, d = be.act_buffer(1, K), be.dst_buffer(1, 2, R)
     args = (K, R, n, 1, 1, 1, eb, eb * n, 1, 2, 8, 2 * R, 8, R, 2, be.stream)
-    # the first call creates the global stats/clock (3 regions); measure the live regions after that
+    # the first call creates the globals (stats, clock, pinned stats, stamps arenas); measure after that
     assert sim.ggml_hip_moe_cache_mul_mat_vec_q(C.byref(t), None, None, y, ids_p, d, *args) == 0
     assert sim.ggml_hip_moe_cache_reset() == 0
     assert sim.ggml_hip_moe_cache_configure(C.byref(cfg)) == 0
@@ -116,8 +156,8 @@ def test_sim_failed_registration_leaves_nothing(sim, mc, tmp_path, fail_after, w
     sim.mc_sim_fail_h2d_after(-1)
     assert rc < 0 and what in sim.ggml_hip_moe_last_error()
     assert sim.ggml_hip_moe_cache_num_entries() == 0
-    # stats/clock/pinned stats of this configuration remain; nothing of the failed entry does
-    assert sim.mc_sim_live_regions() == base + 3
+    # stats/clock/pinned stats and the stamps arena (device + pinned) remain; nothing of the failed entry does
+    assert sim.mc_sim_live_regions() == base + 5
     assert sim.ggml_hip_moe_cache_mul_mat_vec_q(C.byref(t), None, None, y, ids_p, d, *args) == 0
     assert sim.ggml_hip_moe_cache_num_entries() == 1
     expert_of = np.empty(4, np.int32)
