@@ -69,7 +69,8 @@ class Layer:
 
 class MoeDecodeModel:
     def __init__(self, torch, n_layers=48, n_experts=512, hidden=4096, ffn=768, n_used=8, wtype=Q2_K,
-                 sh_type=Q4_K, seed=0, device="cuda", residual=True, fused=True, shared_q8=True, act="q8_1"):
+                 sh_type=Q4_K, seed=0, device="cuda", residual=True, fused=True, shared_q8=True, act="q8_1",
+                 mix="pure"):
         self.torch = torch
         self.fused = fused
         # fused plan: the dots run on q8_1 rows (ggml-CUDA's MMVQ activations, the reference's
@@ -82,22 +83,28 @@ class MoeDecodeModel:
         self.shared_q8 = shared_q8
         self.L, self.E, self.H, self.F, self.U = n_layers, n_experts, hidden, ffn, n_used
         self.wtype, self.sh_type = wtype, sh_type
+        # "pure": every routed matrix in wtype; "q2_K_s": llama.cpp's Q2_K_S expert mix -- the
+        # ffn_down experts of the first n_layer / 8 layers in Q4_K, the rest in wtype
+        assert mix in ("pure", "q2_K_s")
+        self.mix = mix
+        self.down_types = [Q4_K if mix == "q2_K_s" and l < n_layers // 8 else wtype for l in range(n_layers)]
         self.residual = residual
         self.eps = 1e-6
         gen = torch.Generator(device=device)
         gen.manual_seed(seed)
         self.layers = []
         keep = []
-        for _ in range(n_layers):
+        for l in range(n_layers):
             ly = Layer()
+            ly.down_type = self.down_types[l]
             ly.gate = random_expert_tensor(torch, wtype, n_experts, ffn, hidden, gen, device)
             ly.up = random_expert_tensor(torch, wtype, n_experts, ffn, hidden, gen, device)
-            ly.down = random_expert_tensor(torch, wtype, n_experts, hidden, ffn, gen, device)
+            ly.down = random_expert_tensor(torch, ly.down_type, n_experts, hidden, ffn, gen, device)
             ly.sh_gate = random_expert_tensor(torch, sh_type, 1, ffn, hidden, gen, device)[0]
             ly.sh_up = random_expert_tensor(torch, sh_type, 1, ffn, hidden, gen, device)[0]
             ly.sh_down = random_expert_tensor(torch, sh_type, 1, hidden, ffn, gen, device)[0]
             ly.t_up = make_tensor(wtype, hidden, ffn, n_experts, ly.up.data_ptr(), keep=keep)
-            ly.t_down = make_tensor(wtype, ffn, hidden, n_experts, ly.down.data_ptr(), keep=keep)
+            ly.t_down = make_tensor(ly.down_type, ffn, hidden, n_experts, ly.down.data_ptr(), keep=keep)
             self.layers.append(ly)
         self._keep = keep
         f32, u8, i32 = torch.float32, torch.uint8, torch.int32
@@ -132,9 +139,12 @@ class MoeDecodeModel:
             return w + 2 * H * 4 + (U + 1) * F * 4 + (U + 1 if self.shared_q8 else U) * F // 32 * 36
         return w + H // 32 * 36 + (U + 1) * F * 4      # q8_1 row in, GLU rows out
 
-    def down_bytes(self):
+    def down_bytes(self, l=None):
+        """Bytes of layer l's down launch (l None: the mean over the layers)."""
+        if l is None:
+            return sum(self.down_bytes(k) for k in range(self.L)) // self.L
         H, F, U = self.H, self.F, self.U
-        w = U * row_bytes(self.wtype, F) * H + row_bytes(self.sh_type, F) * H
+        w = U * row_bytes(self.down_types[l], F) * H + row_bytes(self.sh_type, F) * H
         if self.fused and self.act == "q8_K":          # fp32 GLU rows, residual, router weights in; x out
             return w + (U + 1) * F * 4 + 2 * H * 4 + U * 4
         if self.fused:                                 # q8_1 (+ fp32 shared) GLU rows, residual, router weights in; x out
@@ -147,7 +157,7 @@ class MoeDecodeModel:
         return 0 if self.fused else (U + 1) * H * 4 + 2 * H * 4 + H * 4 + H // 32 * 36 + U * 4
 
     def bytes_per_token(self):
-        return self.L * (self.gate_up_bytes() + self.down_bytes() + self.combine_bytes())
+        return sum(self.gate_up_bytes() + self.down_bytes(l) + self.combine_bytes() for l in range(self.L))
 
     def _stream(self):
         return C.c_void_p(self.torch.cuda.current_stream().cuda_stream)

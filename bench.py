@@ -139,15 +139,16 @@ def load_traffic(fused):
 
 
 def cpu_baseline(torch, model, ids, w, budget_s=10.0, budget_1t_s=4.0, budget_scalar_s=4.0):
-    """ggml-CPU MUL_MAT_ID restatement (oracle) over layer 0's weights, on this host's cores: AVX2 q8_K vec_dot
-    (bit-identical to the scalar restatement) on all of them, then on one thread, then the scalar vec_dot on
-    all of them."""
+    """ggml-CPU MUL_MAT_ID restatement (oracle) over the last layer's weights (the mix's majority types), on
+    this host's cores: AVX2 q8_K vec_dot (bit-identical to the scalar restatement) on all of them, then on one
+    thread, then the scalar vec_dot on all of them."""
     sys.path.insert(0, str(ROOT))
     from oracle import oracle as O
     nth = int(os.environ.get("OMP_NUM_THREADS", "0")) or O.cpu_cores()
-    ly = model.layers[0]
+    li = model.L - 1
+    ly = model.layers[li]
     mats = tuple(t.cpu().numpy() for t in (ly.gate, ly.up, ly.down, ly.sh_gate, ly.sh_up, ly.sh_down))
-    layer_bytes = model.bytes_per_token() / model.L
+    layer_bytes = model.gate_up_bytes() + model.down_bytes(li) + model.combine_bytes()
     O.set_simd(True)
     n, el = _cpu_layer_loop(O, model, mats, ids, w, nth, budget_s)
     n1, el1 = _cpu_layer_loop(O, model, mats, ids, w, 1, budget_1t_s)
@@ -156,7 +157,7 @@ def cpu_baseline(torch, model, ids, w, budget_s=10.0, budget_1t_s=4.0, budget_sc
     O.set_simd(True)
     gbs = lambda k, t: round(k * layer_bytes / t / 1e9, 3)
     return {"value": gbs(n, el), "unit": "GB/s", "cores": nth, "kind": "port",
-            "sample": f"{n} layer-tokens of the same MoE layer (512 experts Q2_K gate/up/down + Q4_K shared, B=1, "
+            "sample": f"{n} layer-tokens of one MoE layer (512 experts Q2_K gate/up/down + Q4_K shared, B=1, "
                       f"fresh top-8 routing each) through the oracle's ggml-CPU MUL_MAT_ID restatement: q8_K "
                       f"activations, AVX2 vec_dot (bit-identical to the scalar restatement), chunked rows over "
                       f"{nth} OpenMP threads, GLU/combine unfused; {el:.1f} s",
@@ -185,7 +186,8 @@ def _cpu_layer_loop(O, model, mats, ids, w, nth, budget_s):
         shu = O.cpu_mul_mat_id_f32(wtype=model.sh_type, K=H, R=F, n_as=1, src0=su[None], src1=x, ids=one, nthreads=nth)
         hh = (u / (1.0 + np.exp(-g)) * g).reshape(1, U, F).astype(np.float32)        # SwiGLU up*silu(gate)
         hs = (shu / (1.0 + np.exp(-shg)) * shg).reshape(1, F).astype(np.float32)
-        o = O.cpu_mul_mat_id_f32(wtype=model.wtype, K=F, R=H, n_as=E, src0=down, src1=hh, ids=tid, nthreads=nth)
+        o = O.cpu_mul_mat_id_f32(wtype=model.down_types[-1], K=F, R=H, n_as=E, src0=down, src1=hh, ids=tid,
+                                 nthreads=nth)
         os_ = O.cpu_mul_mat_id_f32(wtype=model.sh_type, K=F, R=H, n_as=1, src0=sd[None], src1=hs, ids=one, nthreads=nth)
         x = (x + os_[:, 0] + (w[n % len(w), 0][None, :, None] * o).sum(1)).astype(np.float32)
         x /= max(1.0, float(np.abs(x).max()))
@@ -453,6 +455,9 @@ def main():
     ap.add_argument("--shared-rows", choices=("q8_1", "f32"), default="q8_1",
                     help="fused plan: the gate/up launch writes the shared expert's q8_1 row (q8_1), or only its "
                          "fp32 row, quantized by the down launch, with byte-balanced shared workgroups (f32)")
+    ap.add_argument("--mix", choices=("q2_K_s", "pure"), default="q2_K_s",
+                    help="routed expert types: llama.cpp's Q2_K_S mix (the first n_layer/8 layers' ffn_down in "
+                         "Q4_K, the rest Q2_K; default) or Q2_K everywhere")
     ap.add_argument("--act", choices=("q8_1", "q8_K"), default="q8_1",
                     help="fused plan: the dots' activations, q8_1 (ggml-CUDA MMVQ, the reference's path) or q8_K "
                          "(ggml-CPU MUL_MAT_ID for K-quant experts)")
@@ -490,7 +495,7 @@ def main():
     t0 = time.perf_counter()
     fused = args.plan == "fused"
     model = md.MoeDecodeModel(torch, n_layers=args.layers, fused=fused, shared_q8=args.shared_rows == "q8_1",
-                              act=args.act if fused else "q8_1")
+                              act=args.act if fused else "q8_1", mix=args.mix)
     torch.cuda.synchronize()
     log(f"weights ready: {args.layers} layers in {time.perf_counter() - t0:.1f}s, "
         f"{torch.cuda.memory_allocated() / 2**30:.1f} GiB allocated")
@@ -595,7 +600,11 @@ def main():
         "dtype": "int8",
         "data": "synthetic (random valid Q2_K/Q4_K blocks, N(0,1) input, uniform top-8, softmax router weights)",
         "config": {"workload": f"{model.L}-layer MoE decode step, B=1: 512 experts, hidden 4096, expert ffn 768, "
-                               "top-8, Q2_K routed gate/up/down + Q4_K shared expert, fused SwiGLU, all resident",
+                               "top-8, " + ("Q2_K_S expert mix (Q2_K gate/up, Q2_K down except the first "
+                                            f"{model.L // 8} layers' in Q4_K)" if model.mix == "q2_K_s" else
+                                            "Q2_K routed gate/up/down") +
+                               " + Q4_K shared expert, fused SwiGLU, all resident",
+                   "mix": model.mix,
                    "layers": model.L, "experts": model.E, "hidden": model.H, "ffn": model.F, "top_k": model.U,
                    "routed_type": "q2_K", "shared_type": "q4_K", "batch": 1,
                    "plan": f"{args.plan}: {2 if fused else 3} launches per layer",

@@ -535,13 +535,19 @@ def test_down_combine_q8K(torch_gpu, mc, O, wtype, sh_type, K, R, n_tok, U, resi
     assert O.rel_l2(x_out.cpu().numpy(), want_x) <= 1e-5
 
 
-def test_fused_q8K_decode_against_ggml_cpu(torch_gpu, mc, O):
+@pytest.mark.parametrize("n_layers,mix", [(2, "pure"), (8, "q2_K_s")])
+def test_fused_q8K_decode_against_ggml_cpu(torch_gpu, mc, O, n_layers, mix):
     """The headline decode block in q8_K mode against the ggml-CPU MUL_MAT_ID restatement
     (fp32 src1 quantized to q8_K inside, K-quant x q8_K dots), op by op: RMSNorm, gate/up +
-    SwiGLU, down, router-weighted combine with the shared expert and the residual."""
+    SwiGLU, down, router-weighted combine with the shared expert and the residual.  q2_K_s:
+    the first n_layers / 8 layers' down experts in Q4_K."""
     torch = torch_gpu
     md = import_module("a6000_custom_kernels_amd.moe_decode")
-    m = md.MoeDecodeModel(torch, n_layers=2, n_experts=32, hidden=2048, ffn=768, n_used=8, seed=12, act="q8_K")
+    _note(f"q8_K decode {n_layers} layers, mix {mix}")
+    m = md.MoeDecodeModel(torch, n_layers=n_layers, n_experts=32, hidden=2048, ffn=768, n_used=8, seed=12, act="q8_K",
+                          mix=mix)
+    if mix == "q2_K_s":
+        assert m.down_types[0] == mc.Q4_K and m.down_types[1] == m.wtype
     H, F, U, E = m.H, m.F, m.U, m.E
     ids, w = md.make_routing(1, m.L, E, U, seed=4)
     x0 = (np.random.default_rng(13).standard_normal((1, H)) * 2).astype(np.float32)
@@ -566,7 +572,7 @@ def test_fused_q8K_decode_against_ggml_cpu(torch_gpu, mc, O):
         glu = np.vectorize(lambda a, b: O.glu(O.GLU_SWIGLU, float(a), float(b), 0.0), otypes=[np.float32])
         hh = glu(g, u).reshape(1, U, F)
         hs = glu(sg, su).reshape(1, 1, F)
-        o = cpu(m.wtype, ly.down, F, H, E, hh, lid)
+        o = cpu(ly.down_type, ly.down, F, H, E, hh, lid)
         osh = cpu(m.sh_type, ly.sh_down, F, H, 1, hs, z).reshape(1, H)
         x, _ = O.combine_q8_1(o.reshape(1, U, H), w[0, l].reshape(1, U), shared=osh, residual=x)
     err = O.rel_l2(got, x)
