@@ -669,7 +669,13 @@ int gemv_common(int use_cache, int act, const ggml_hip_moe_tensor *src0, const g
     if (ne00 <= 0 || ne01 <= 0 || ne02 <= 0 || ncols_dst <= 0 || nchannels_dst <= 0 || nchannels_y <= 0)
         return fail(E_INVALID, "moe-gemv: empty shape");
     if (ne00 % g.unit_elems) return fail(E_UNSUPPORTED, "moe-gemv: ne00=%lld is not a multiple of %d", (long long) ne00, g.unit_elems);
-    if (ne00 / g.unit_elems > WAVE) return fail(E_UNSUPPORTED, "moe-gemv: ne00=%lld exceeds %d units per row", (long long) ne00, WAVE);
+    // the plain GEMV streams rows of more than 64 units in chunks; the fused decode kernels
+    // hold one row per step (at most 64 units)
+    if (mode != FFN_NONE && ne00 / g.unit_elems > WAVE)
+        return fail(E_UNSUPPORTED, "moe-ffn: ne00=%lld exceeds %d units per row", (long long) ne00, WAVE);
+    if (ne00 > GEMV_MAX_K || (act == ACT_F32 && ne00 > GEMV_MAX_K_F32))
+        return fail(E_UNSUPPORTED, "moe-gemv: ne00=%lld exceeds the staged activation row (%d values, %d for fp32 rows)",
+                    (long long) ne00, GEMV_MAX_K, GEMV_MAX_K_F32);
     if (src0->ne[0] != ne00 || src0->ne[1] != ne01 || src0->ne[2] != ne02 || !is_contiguous(src0))
         return fail(E_INVALID, "moe-gemv: src0 shape/strides do not match the call");
     if (act != ACT_Q8_1 && act != ACT_Q8_K && act != ACT_F32)
@@ -685,7 +691,7 @@ int gemv_common(int use_cache, int act, const ggml_hip_moe_tensor *src0, const g
     if (sh_up) {
         ts = fusion->shared_type < 0 ? tw : fusion->shared_type;
         if (!type_supported(ts)) return fail(E_UNSUPPORTED, "moe-gemv: unsupported shared-expert type %d", ts);
-        if (ne00 % type_geom(ts).unit_elems || ne00 / type_geom(ts).unit_elems > WAVE)
+        if (ne00 % type_geom(ts).unit_elems || (mode != FFN_NONE && ne00 / type_geom(ts).unit_elems > WAVE))
             return fail(E_UNSUPPORTED, "moe-gemv: shared-expert row length not supported");
         if (act == ACT_Q8_K && !type_geom(ts).kquant) return fail(E_UNSUPPORTED, "moe-gemv: q8_K activations need a K-quant shared expert");
         if (!fusion->shared_dst && mode != FFN_DOWN_COMBINE) return fail(E_INVALID, "moe-gemv: shared_up without shared_dst");

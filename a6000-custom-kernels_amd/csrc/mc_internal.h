@@ -183,6 +183,10 @@ constexpr uint32_t FFN_LDS_MAX = 160 * 1024;
 // LDS a GEMV workgroup may use, chosen so that 8 workgroups fit one CU's
 // 160 KiB: a decode launch of ~2000 single-wave tiles is then resident at once.
 constexpr uint32_t GEMV_LDS_BUDGET = 20 * 1024;
+// Longest row of the plain GEMV: its activation row (and, for fp32 rows, the q8_1 copy) is
+// staged in LDS beside two 64-unit spans, within FFN_LDS_MAX.
+constexpr int GEMV_MAX_K = 65536;
+constexpr int GEMV_MAX_K_F32 = 16384;
 
 inline constexpr uint32_t round_up_1k(uint32_t b) { return (b + 1023u) & ~1023u; }
 

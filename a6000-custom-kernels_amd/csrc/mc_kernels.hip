@@ -32,10 +32,52 @@ namespace mc {
 // ---------------------------------------------------------------------------
 // one step of one matrix pair (up [+ gate]) for one pick (mc_step.h)
 // ---------------------------------------------------------------------------
+
+// A row of more than 64 units (legacy types above K = 4096, K-quants above 16384):
+// the step is that one row, streamed through the spans in chunks of 64 units; lane l
+// dots unit 64j + l of chunk j and keeps its own sum, the 64 lane sums are added at
+// the end (a fixed order).  On entry the activation row (q8_1 or q8_K blocks) is in
+// LDS at arow with, for q8_1, its 16-value sums at rs16; the expert is resolved.
+template <int T, int AQ>
+__device__ __forceinline__ void wide_row_dots(const GemvArgs &a, StepCtx &s, uint8_t *lds, const uint8_t *arow,
+                                              const int16_t *rs16, float &su, float &sg) {
+    constexpr TypeGeom G = type_geom(T);
+    constexpr int UE = G.unit_elems;
+    constexpr int AUB = AQ == ACT_Q8_1 ? UE / 32 * 36 : 292;
+    const int lane = threadIdx.x % WAVE;
+    const int nu = a.ncols / UE;
+    const u32 mbytes = (u32) (s.shared ? a.sh_matrix_bytes : a.expert_bytes);
+    const u32 row_start = (u32) s.row0 * (u32) nu * (u32) G.unit_bytes;
+    float pu = 0.0f, pg = 0.0f;
+    for (int c0 = 0; c0 < nu; c0 += WAVE) {
+        const int nuc = min(WAVE, nu - c0);
+        const u32 start = row_start + (u32) c0 * (u32) G.unit_bytes;
+        const u32 nbytes = (u32) nuc * (u32) G.unit_bytes;
+        // the previous chunk's LDS reads have all returned (their values were used): the spans are free
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (s.wgate) dma_span<T>(s.wgate, mbytes, start, nbytes, lds + a.lds_span);
+        const int n_up = dma_span<T>(s.wup, mbytes, start, nbytes, lds);
+        const bool active = lane < nuc;
+        const int col = c0 + lane;
+        Act<UE> A;
+        const int16_t *us16 = AQ == ACT_Q8_1 ? rs16 + (u32) col * (UE / 16) : nullptr;
+        if (active) load_act_lds<UE, AQ, AQ == ACT_Q8_1>(A, arow + (u32) col * AUB, us16);
+        if (s.wgate) {
+            wait_loads_at_most(n_up);
+            if (active) pg += span_unit_dot<T, AQ>(lds + a.lds_span, span_lead(s.wgate, start), lane, A);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (active) pu += span_unit_dot<T, AQ>(lds, span_lead(s.wup, start), lane, A);
+    }
+    su = row_group_sum(pu, WAVE);
+    sg = s.wgate ? row_group_sum(pg, WAVE) : 0.0f;
+}
+
 template <int T, int ACT>
 __device__ __forceinline__ void run_step(const GemvArgs &a, uint8_t *lds, bool shared, int tile) {
     constexpr int AQ = ACT == ACT_F32 ? ACT_Q8_1 : ACT;          // block format the dots read
     StepCtx s = step_locate(a, shared, tile);
+    const bool wide = a.ncols / type_geom(T).unit_elems > WAVE;
     // the activation row depends only on (token, slot): its DMA goes out first
     const uint8_t *ybase;
     u32 yrow, ybytes;
@@ -53,7 +95,8 @@ __device__ __forceinline__ void run_step(const GemvArgs &a, uint8_t *lds, bool s
         yrow = (u32) ((int64_t) s.t * a.stride_col_y);
     }
     const u32 alead = dma_bytes(ybase, ybytes, yrow, a.act_row_bytes, lds + a.lds_act);
-    step_issue<T>(a, s, lds);
+    if (wide) step_resolve(a, s);                          // the chunks are streamed by wide_row_dots
+    else step_issue<T>(a, s, lds);
     if (!s.valid) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         return;
@@ -67,7 +110,11 @@ __device__ __forceinline__ void run_step(const GemvArgs &a, uint8_t *lds, bool s
         arow = lds + a.lds_q8;
     }
     float su, sg;
-    if constexpr (AQ == ACT_Q8_1) {
+    if (wide) {
+        int16_t *rs16 = (int16_t *) (lds + a.lds_sums);
+        if constexpr (AQ == ACT_Q8_1) row_sums16_lds(arow, a.ncols, rs16);
+        wide_row_dots<T, AQ>(a, s, lds, arow, rs16, su, sg);
+    } else if constexpr (AQ == ACT_Q8_1) {
         // the row's 16-value code sums, once per wave (min / offset terms of the dots)
         int16_t *rs16 = (int16_t *) (lds + a.lds_sums);
         row_sums16_lds(arow, a.ncols, rs16);
@@ -267,6 +314,11 @@ __global__ __launch_bounds__(COMBINE_THREADS) void mc_combine_q8_1_kernel(const 
 
 template <int TW, int TS, int ACT>
 static hipError_t launch_t(const GemvArgs &a, hipStream_t s) {
+    // rows of more than 16K values stage activation rows beyond the default 64 KiB of LDS
+    if (a.lds_total > 64u * 1024u) {
+        static_cast<void>(hipFuncSetAttribute((const void *) mc_gemv_kernel<TW, TS, ACT>,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int) FFN_LDS_MAX));
+    }
     hipLaunchKernelGGL((mc_gemv_kernel<TW, TS, ACT>), dim3((unsigned) (a.n_tiles + a.rec)), dim3(WAVE),
                        a.lds_total, s, a);
     return hipGetLastError();
@@ -335,19 +387,21 @@ int launch_gemv(GemvArgs a, int tw, int ts, int act, void *stream) {
     const uint32_t act_span = round_up_1k(a.act_row_bytes + 20u) + q8_bytes + sums_bytes;
     if (ts == 0 || !a.sh_up) ts = 0;
     const int nspan = (a.has_gate || (ts != 0 && a.sh_gate)) ? 2 : 1;
-    a.rps = fit_rows_per_step(nu, rb, nspan, act_span);
+    // a row of more than 64 units is one step, staged 64 units at a time (wide_row_dots)
+    a.rps = nu > WAVE ? 1 : fit_rows_per_step(nu, rb, nspan, act_span);
     a.tiles_per_pick = (a.nrows + a.rps - 1) / a.rps;
     a.n_routed_tiles = a.tiles_per_pick * a.n_used * a.n_tok;
-    uint32_t span = span_bytes((uint32_t) a.rps, rb);
+    uint32_t span = nu > WAVE ? span_bytes(1u, (uint32_t) WAVE * (uint32_t) g.unit_bytes) : span_bytes((uint32_t) a.rps, rb);
     a.sh_rps = 0;
     a.sh_tiles_per_tok = 0;
     if (ts != 0) {
         const TypeGeom gs = type_geom(ts);
         const int nus = a.ncols / gs.unit_elems;
         const uint32_t rbs = (uint32_t) nus * (uint32_t) gs.unit_bytes;
-        a.sh_rps = fit_rows_per_step(nus, rbs, nspan, act_span);
+        a.sh_rps = nus > WAVE ? 1 : fit_rows_per_step(nus, rbs, nspan, act_span);
         a.sh_tiles_per_tok = (a.nrows + a.sh_rps - 1) / a.sh_rps;
-        const uint32_t sspan = span_bytes((uint32_t) a.sh_rps, rbs);
+        const uint32_t sspan = nus > WAVE ? span_bytes(1u, (uint32_t) WAVE * (uint32_t) gs.unit_bytes)
+                                          : span_bytes((uint32_t) a.sh_rps, rbs);
         span = sspan > span ? sspan : span;
     }
     a.lds_span = span;
@@ -355,6 +409,7 @@ int launch_gemv(GemvArgs a, int tw, int ts, int act, void *stream) {
     a.lds_q8 = a.lds_act + act_span - q8_bytes - sums_bytes;
     a.lds_sums = a.lds_act + act_span - sums_bytes;
     a.lds_total = a.lds_act + act_span;
+    if (a.lds_total > FFN_LDS_MAX) return (int) hipErrorInvalidValue;
     a.rec = (a.stats || a.stamps || a.stamps_gate) ? 1 : 0;
     a.n_tiles = a.n_routed_tiles + a.sh_tiles_per_tok * a.n_tok;
     if (a.n_tiles <= 0) return (int) hipSuccess;

@@ -24,8 +24,13 @@
  * cannot be built here): tests/test_oracle_formats.py and
  * tests/test_oracle_mmid.py -- hand-built known-answer blocks, closed-form
  * special cases, integer-sum identities, fp64 dequantized dot products and
- * brute force on tiny inputs.  Items marked "parity unpinned" in
- * oracle/README.md have no such check.
+ * brute force on tiny inputs.  The two GLU ops the reference calls without
+ * defining (SWIGLU_OAI, SWIGLU_CLAMP) are checked against the gpt-oss and
+ * DeepSeek-V4 model definitions of the transformers package
+ * (tests/test_oracle_glu_models.py).  Parity unpinned: only what no function
+ * here restates -- the rounding of upstream ggml-CUDA's own vec_dot_*_q8_1
+ * kernels, which the GEMV does not follow bit for bit (it follows the CPU
+ * integer-offset formulation restated here).
  */
 #ifndef MC_ORACLE_H
 #define MC_ORACLE_H
