@@ -1074,31 +1074,43 @@ __device__ __forceinline__ void q8K_chunks(const float (&v)[N][4], uint8_t *cons
 // multiple, so every block is read with 128-bit LDS reads.
 constexpr int Q8K_LDS_STRIDE = 304;
 
-__device__ __forceinline__ void quantize_row_lds_q8K(const float *x, uint8_t *q, int k) {
-    constexpr int G = 4;                                   // blocks interleaved per pass
+// G blocks b0 .. b0 + G - 1 of quantize_row_lds_q8K, interleaved.
+template <int G>
+__device__ __forceinline__ void q8K_row_blocks(const float *x, uint8_t *q, int b0, bool al) {
     const int lane = threadIdx.x % WAVE;
+    float v[G][4];
+    uint8_t *yb[G];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        const float *src = x + 256 * (b0 + i) + 4 * lane;
+        if (al) {
+            const v4f x4 = *(const v4f *) __builtin_assume_aligned(src, 16);
+            v[i][0] = x4.x;
+            v[i][1] = x4.y;
+            v[i][2] = x4.z;
+            v[i][3] = x4.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[i][j] = src[j];
+        }
+        yb[i] = q + Q8K_LDS_STRIDE * (b0 + i);
+    }
+    q8K_chunks<G>(v, yb, yb, false);
+}
+
+// The wave's fp32 row of k values (k a multiple of 256) as q8_K blocks, Q8K_LDS_STRIDE
+// apart: four blocks per pass, then the remaining one to three together (a 768-value row
+// is one pass of three), so no block is quantized twice.
+__device__ __forceinline__ void quantize_row_lds_q8K(const float *x, uint8_t *q, int k) {
     const bool al = ((uintptr_t) x & 15u) == 0;
     const int nblk = k / 256;
-    for (int b0 = 0; b0 < nblk; b0 += G) {
-        float v[G][4];
-        uint8_t *yb[G];
-#pragma unroll
-        for (int i = 0; i < G; ++i) {
-            const int b = min(b0 + i, nblk - 1);           // past the row: the last block again, same bytes
-            const float *src = x + 256 * b + 4 * lane;
-            if (al) {
-                const v4f x4 = *(const v4f *) __builtin_assume_aligned(src, 16);
-                v[i][0] = x4.x;
-                v[i][1] = x4.y;
-                v[i][2] = x4.z;
-                v[i][3] = x4.w;
-            } else {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) v[i][j] = src[j];
-            }
-            yb[i] = q + Q8K_LDS_STRIDE * b;
-        }
-        q8K_chunks<G>(v, yb, yb, false);
+    int b0 = 0;
+    for (; b0 + 4 <= nblk; b0 += 4) q8K_row_blocks<4>(x, q, b0, al);
+    switch (nblk - b0) {
+        case 3: q8K_row_blocks<3>(x, q, b0, al); break;
+        case 2: q8K_row_blocks<2>(x, q, b0, al); break;
+        case 1: q8K_row_blocks<1>(x, q, b0, al); break;
+        default: break;
     }
     wave_lds_sync();
 }

@@ -3,9 +3,10 @@
 
 Workload (one "step" = one decode token): the MoE block of a 48-layer model
 shaped like the reference's (512 experts, hidden 4096, expert FFN 768, top-8
-routing with softmax router weights, Q2_K routed experts, one always-on Q4_K
-shared expert, fused SwiGLU), batch 1, every layer with its own weights
-(~76 GB resident in HBM, so the 256 MB MALL cannot serve repeat reads).  One
+routing with softmax router weights, llama.cpp's Q2_K_S expert mix (Q2_K, the
+first 6 layers' ffn_down in Q4_K), one always-on Q4_K shared expert, fused
+SwiGLU), batch 1, every layer with its own weights (73 GiB resident in HBM, so
+the 256 MB MALL cannot serve repeat reads).  One
 token = 2 launches per layer through the C ABI (--plan fused: gate/up GEMV with
 the RMSNorm + q8_1 of its input in the same launch, then the down GEMV with the
 weighted combine), or 3 per layer (--plan ops: gate/up, down, combine),
@@ -424,8 +425,27 @@ def wl_table_gate_up(torch, mc, md, rounds, layers=8, routings=4):
     return out
 
 
+def wl_cache_mixed(torch, mc, md, rounds, layers=40, tokens=128, calib_tokens=16):
+    """The pointer-table cache under mixed residency (bench_configs.cfg3_runs): Q2_K gate/up/down experts of up
+    to 40 layers (as many as the host lets the GPU map) in pinned host memory, a 435/512 HBM pool per tensor,
+    Zipf(1.1) routing, the cache step between tokens; all-hit and all-miss calibrations beside it."""
+    sys.path.insert(0, str(ROOT))
+    from bench_configs import cfg3_runs
+    hit, miss, mix = cfg3_runs(torch, mc, md, tokens=tokens, calib_tokens=calib_tokens, layers=layers,
+                               async_run=False)
+    torch.cuda.empty_cache()
+    keys = ("tokens", "hit_rate", "promotions", "us_per_token_gpu", "us_per_token_step", "us_per_token_wall",
+            "tok_per_s_gpu", "tok_per_s_with_step", "HBM_GB/s_hits", "PCIe_GB/s_misses", "us_per_layer_gpu")
+    return {"workload": f"pointer-table cache under mixed residency: {mix['layers']} layers of 512 Q2_K gate/up/down "
+                        "experts (hidden 4096, ffn 768) in pinned host memory, 435/512 per tensor in the HBM pool "
+                        "(seeded), Zipf(1.1) top-8 routing, B=1, miss log + LRU step (48 promotions) between tokens",
+            "layers": mix["layers"], **{k: mix[k] for k in keys},
+            "calibration": {"all_hit_HBM_GB/s": hit["HBM_GB/s"], "all_hit_us_per_token": hit["us_per_token_gpu"],
+                            "all_miss_PCIe_GB/s": miss["PCIe_GB/s"], "all_miss_us_per_token": miss["us_per_token_gpu"]}}
+
+
 WORKLOADS = {"decode_q4_0": wl_decode_q4_0, "type_batch": wl_type_batch, "prefill": wl_prefill,
-             "table_gate_up": wl_table_gate_up}
+             "cache_mixed": wl_cache_mixed, "table_gate_up": wl_table_gate_up}
 
 
 def run_workloads(torch, mc, md, names, args):
@@ -437,7 +457,9 @@ def run_workloads(torch, mc, md, names, args):
         res[name] = fn(torch, mc, md, args.kernel_rounds) if name != "decode_q4_0" else \
             fn(torch, mc, md, args.kernel_rounds, cpu_s=0.0 if args.no_cpu else 3.0)
         r = res[name]
-        log(f"workload {name}: " + (f"{r['us']} us, {r['GB/s']} GB/s" if "us" in r else "done") +
+        log(f"workload {name}: " + (f"{r['us']} us, {r['GB/s']} GB/s" if "us" in r else
+                                     f"hit rate {r['hit_rate']}, {r['us_per_token_wall']} us/token with the step"
+                                     if "hit_rate" in r else "done") +
             f" ({time.perf_counter() - t0:.1f}s)")
     return res
 

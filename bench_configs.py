@@ -35,6 +35,7 @@ import ctypes as C
 import json
 import os
 import sys
+import tempfile
 import time
 from importlib import import_module
 from pathlib import Path
@@ -263,17 +264,19 @@ def _hip_runtime(torch):
     lib = C.CDLL(os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so"))
     lib.hipHostMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t, C.c_uint]
     lib.hipHostMalloc.restype = C.c_int
+    lib.hipHostFree.argtypes = [C.c_void_p]
+    lib.hipHostFree.restype = C.c_int
     lib.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
     lib.hipMemcpy.restype = C.c_int
     return lib
 
 
-def cfg3(torch, mc, md, rounds, tokens=256, calib_tokens=32, layers=40):
-    """Pointer-table cache under mixed residency: 40 layers (the GPU-mappable pinned host memory
-    of the measurement box ends near 70 GB; 48 layers need 76 GB) of Q2_K gate/up/down experts in
-    pinned host memory, an HBM pool of 435 of each tensor's 512 experts seeded from the head of
-    a seeded per-layer permutation, Zipf(1.1) routing over that permutation, the cache step
-    (miss log, LRU promotion) between tokens.  Calibrated by an all-hit and an all-miss run."""
+def cfg3_runs(torch, mc, md, tokens=256, calib_tokens=32, layers=40, min_layers=8, async_run=True):
+    """Pointer-table cache under mixed residency: up to `layers` layers of Q2_K gate/up/down experts in
+    pinned host memory (as many as the host lets the GPU map, at least min_layers), an HBM pool of 435 of
+    each tensor's 512 experts seeded from the head of a seeded per-layer permutation, Zipf(1.1) routing over
+    that permutation, the cache step (miss log, LRU promotion) between tokens.  Calibrated by an all-hit and
+    an all-miss run (the latter measures the zero-copy PCIe rate directly).  Returns the runs' records."""
     import numpy as np
     E, H, F, U, POOL = 512, 4096, 768, 8, 435
     t = mc.Q2_K
@@ -284,18 +287,31 @@ def cfg3(torch, mc, md, rounds, tokens=256, calib_tokens=32, layers=40):
     hip = _hip_runtime(torch)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(41)
-    keep, tens = [], {}
+    keep, tens, pinned = [], {}, []
     t0 = time.perf_counter()
     for l in range(layers):
+        got = []
         for role, rows, k in (("gate", F, H), ("up", F, H), ("down", H, F)):
             p = C.c_void_p()
-            rc = hip.hipHostMalloc(C.byref(p), E * eb, 0)
-            assert rc == 0, f"hipHostMalloc of {E * eb} bytes returned {rc} after {len(tens)} tensors"
+            if hip.hipHostMalloc(C.byref(p), E * eb, 0) != 0:
+                break
+            got.append((role, rows, k, p))
+        if len(got) < 3:                             # the host maps no more: keep the whole layers so far
+            for _, _, _, p in got:
+                hip.hipHostFree(p)
+            layers = l
+            break
+        for role, rows, k, p in got:
+            pinned.append(p)
             dev = md.random_expert_tensor(torch, t, E, rows, k, gen)
             torch.cuda.synchronize()
             assert hip.hipMemcpy(p, C.c_void_p(dev.data_ptr()), E * eb, 2) == 0, "hipMemcpy D2H"
             del dev
             tens[(l, role)] = mc.make_tensor(t, k, rows, E, p.value, name=f"blk.{l}.ffn_{role}_exps.weight", keep=keep)
+    if layers < min_layers:
+        for p in pinned:
+            hip.hipHostFree(p)
+        raise RuntimeError(f"cfg3: only {layers} layers of pinned host memory could be mapped")
     log(f"cfg3: {3 * layers} expert tensors ({3 * layers * E * eb / 2**30:.1f} GiB) in pinned host memory, "
         f"{time.perf_counter() - t0:.1f}s")
     rng = np.random.default_rng(42)
@@ -326,6 +342,7 @@ def cfg3(torch, mc, md, rounds, tokens=256, calib_tokens=32, layers=40):
     o = torch.zeros((U, H), dtype=torch.float32, device="cuda")
     ids_dev = torch.zeros((layers, U), dtype=torch.int32, device="cuda")
     ar = H // 32
+    tmpdir = tempfile.mkdtemp()
 
     def token(stream):
         sp = C.c_void_p(stream.cuda_stream)
@@ -339,7 +356,7 @@ def cfg3(torch, mc, md, rounds, tokens=256, calib_tokens=32, layers=40):
 
     def run(tag, slots, n_top, n_tok, max_promotions, async_promotions=False):
         mc.reset()
-        path = seed_file(f"/tmp/moe_seed_{tag}.txt", n_top) if n_top else None
+        path = seed_file(os.path.join(tmpdir, f"moe_seed_{tag}.txt"), n_top) if n_top else None
         mc.configure(enabled=True, slots=slots, budget_gb=0.0, margin_gb=2.0, seed_path=path,
                      max_promotions=max_promotions, async_promotions=async_promotions)
         ids = route(n_tok + 1)
@@ -370,6 +387,7 @@ def cfg3(torch, mc, md, rounds, tokens=256, calib_tokens=32, layers=40):
                 mc.check(lib.ggml_hip_moe_cache_step(C.c_void_p(s.cuda_stream)), "step")
                 step_s += time.perf_counter() - ts
             t_all = time.perf_counter() - t_all
+            del g
         tot = mc.totals()
         hits, misses = tot.hits - base.hits, tot.misses - base.misses
         picks = hits + misses
@@ -379,33 +397,48 @@ def cfg3(torch, mc, md, rounds, tokens=256, calib_tokens=32, layers=40):
                 "us_per_token_step": round(step_s * 1e6 / n_tok, 1), "us_per_token_wall": round(t_all * 1e6 / n_tok, 1),
                 "registration_s": round(t_reg, 2), "bytes_per_token": int(picks / n_tok * eb)}
 
-    hit = run("allhit", E, E, calib_tokens, 0)
-    hit_gbs = hit["bytes_per_token"] / (hit["us_per_token_gpu"] * 1e-6) / 1e9
-    emit({"config": "cfg3", "run": "calibration, every expert in the HBM pool", **hit, "HBM_GB/s": round(hit_gbs, 1)})
-    miss = run("allmiss", 1, 0, calib_tokens, 0)
-    miss_gbs = miss["bytes_per_token"] / (miss["us_per_token_gpu"] * 1e-6) / 1e9
-    emit({"config": "cfg3", "run": "calibration, every expert read zero-copy from pinned host memory", **miss,
-          "PCIe_GB/s": round(miss_gbs, 2)})
-    mix = run("mixed", POOL, POOL, tokens, 48)
-    # time split: hit bytes at the all-hit rate, the rest of the GPU time is spent on misses
-    hit_bytes = mix["hits"] / mix["tokens"] * eb
-    miss_bytes = mix["misses"] / mix["tokens"] * eb
-    t_hit = hit_bytes / (hit_gbs * 1e9)
-    t_miss = max(mix["us_per_token_gpu"] * 1e-6 - t_hit, 1e-9)
-    emit({"config": "cfg3", "run": f"{layers} layers, pool 435/512 per tensor seeded from the permutation head, "
-                                   "Zipf(1.1) routing, miss log + LRU step between tokens", **mix,
-          "layers": layers, "us_per_layer_gpu": round(mix["us_per_token_gpu"] / layers, 2),
-          "HBM_GB/s_hits": round(hit_gbs, 1),
-          "PCIe_GB/s_misses": round(miss_bytes / t_miss / 1e9, 2) if miss_bytes else None,
-          "tok_per_s_gpu": round(1e6 / mix["us_per_token_gpu"], 1),
-          "tok_per_s_with_step": round(1e6 / mix["us_per_token_wall"], 1)})
-    # the same run with the promotion copies on the library's second stream
-    mixa = run("mixed_async", POOL, POOL, tokens, 48, async_promotions=True)
-    emit({"config": "cfg3", "run": f"{layers} layers, as above, promotion copies on a second stream "
-                                   "(async_promotions)", **mixa, "layers": layers,
-          "tok_per_s_gpu": round(1e6 / mixa["us_per_token_gpu"], 1),
-          "tok_per_s_with_step": round(1e6 / mixa["us_per_token_wall"], 1)})
-    mc.reset()
+    out = []
+    try:
+        hit = run("allhit", E, E, calib_tokens, 0)
+        hit_gbs = hit["bytes_per_token"] / (hit["us_per_token_gpu"] * 1e-6) / 1e9
+        out.append({"run": "calibration, every expert in the HBM pool", **hit, "HBM_GB/s": round(hit_gbs, 1)})
+        miss = run("allmiss", 1, 0, calib_tokens, 0)
+        miss_gbs = miss["bytes_per_token"] / (miss["us_per_token_gpu"] * 1e-6) / 1e9
+        out.append({"run": "calibration, every expert read zero-copy from pinned host memory", **miss,
+                    "PCIe_GB/s": round(miss_gbs, 2)})
+        mix = run("mixed", POOL, POOL, tokens, 48)
+        # time split: hit bytes at the all-hit rate, the rest of the GPU time is spent on misses
+        hit_bytes = mix["hits"] / mix["tokens"] * eb
+        miss_bytes = mix["misses"] / mix["tokens"] * eb
+        t_hit = hit_bytes / (hit_gbs * 1e9)
+        t_miss = max(mix["us_per_token_gpu"] * 1e-6 - t_hit, 1e-9)
+        out.append({"run": f"{layers} layers, pool 435/512 per tensor seeded from the permutation head, "
+                           "Zipf(1.1) routing, miss log + LRU step between tokens", **mix,
+                    "layers": layers, "us_per_layer_gpu": round(mix["us_per_token_gpu"] / layers, 2),
+                    "HBM_GB/s_hits": round(hit_gbs, 1),
+                    "PCIe_GB/s_misses": round(miss_bytes / t_miss / 1e9, 2) if miss_bytes else None,
+                    "tok_per_s_gpu": round(1e6 / mix["us_per_token_gpu"], 1),
+                    "tok_per_s_with_step": round(1e6 / mix["us_per_token_wall"], 1)})
+        if async_run:
+            # the same run with the promotion copies on the library's second stream
+            mixa = run("mixed_async", POOL, POOL, tokens, 48, async_promotions=True)
+            out.append({"run": f"{layers} layers, as above, promotion copies on a second stream "
+                               "(async_promotions)", **mixa, "layers": layers,
+                        "tok_per_s_gpu": round(1e6 / mixa["us_per_token_gpu"], 1),
+                        "tok_per_s_with_step": round(1e6 / mixa["us_per_token_wall"], 1)})
+    finally:
+        mc.reset()
+        torch.cuda.synchronize()
+        for p in pinned:
+            hip.hipHostFree(p)
+    return out
+
+
+def cfg3(torch, mc, md, rounds, tokens=256, calib_tokens=32, layers=40):
+    """cfg3_runs at 40 layers (the GPU-mappable pinned host memory of the measurement box ends near
+    70 GB; 48 layers need 76 GB), each record emitted."""
+    for rec in cfg3_runs(torch, mc, md, tokens=tokens, calib_tokens=calib_tokens, layers=layers):
+        emit({"config": "cfg3", **rec})
 
 
 def main():
