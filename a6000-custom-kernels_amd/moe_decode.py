@@ -70,7 +70,7 @@ class Layer:
 class MoeDecodeModel:
     def __init__(self, torch, n_layers=48, n_experts=512, hidden=4096, ffn=768, n_used=8, wtype=Q2_K,
                  sh_type=Q4_K, seed=0, device="cuda", residual=True, fused=True, shared_q8=True, act="q8_1",
-                 mix="pure"):
+                 mix="pure", hand_off="q8_1"):
         self.torch = torch
         self.fused = fused
         # fused plan: the dots run on q8_1 rows (ggml-CUDA's MMVQ activations, the reference's
@@ -81,6 +81,11 @@ class MoeDecodeModel:
         # workgroups) or only its fp32 row, which the down launch quantizes (shared
         # workgroups of a routed one's bytes)
         self.shared_q8 = shared_q8
+        # fused plan, q8_1 dots: the gate/up launch hands the GLU rows over as q8_1 blocks (32-row
+        # workgroups, one q8_1 block each) or as fp32 rows only (workgroups sized by bytes to the CU
+        # count), which every down wave quantizes to q8_1 itself; q8_K dots always take fp32 rows
+        assert hand_off in ("q8_1", "f32")
+        self.hand_off = hand_off
         self.L, self.E, self.H, self.F, self.U = n_layers, n_experts, hidden, ffn, n_used
         self.wtype, self.sh_type = wtype, sh_type
         # "pure": every routed matrix in wtype; "q2_K_s": llama.cpp's Q2_K_S expert mix -- the
@@ -128,12 +133,17 @@ class MoeDecodeModel:
                                    shared_stride_col_y=ffn // 32)
         self.graph = None
 
+    @property
+    def f32_rows(self):
+        """Fused plan: the GLU rows reach the down launch as fp32 rows (q8_K dots, or the fp32 hand-off)."""
+        return self.fused and (self.act == "q8_K" or self.hand_off == "f32")
+
     # Algorithmic bytes: unique expert matrices + shared expert + the activations
     # and outputs each launch of the plan reads or writes once.
     def gate_up_bytes(self):
         H, F, U = self.H, self.F, self.U
         w = U * 2 * row_bytes(self.wtype, H) * F + 2 * row_bytes(self.sh_type, H) * F
-        if self.fused and self.act == "q8_K":          # x row + norm weight in, fp32 GLU rows out
+        if self.f32_rows:                              # x row + norm weight in, fp32 GLU rows out
             return w + 2 * H * 4 + (U + 1) * F * 4
         if self.fused:                                 # x row + norm weight in, GLU rows (fp32 + q8_1) out
             return w + 2 * H * 4 + (U + 1) * F * 4 + (U + 1 if self.shared_q8 else U) * F // 32 * 36
@@ -145,7 +155,7 @@ class MoeDecodeModel:
             return sum(self.down_bytes(k) for k in range(self.L)) // self.L
         H, F, U = self.H, self.F, self.U
         w = U * row_bytes(self.down_types[l], F) * H + row_bytes(self.sh_type, F) * H
-        if self.fused and self.act == "q8_K":          # fp32 GLU rows, residual, router weights in; x out
+        if self.f32_rows:                              # fp32 GLU rows, residual, router weights in; x out
             return w + (U + 1) * F * 4 + 2 * H * 4 + U * 4
         if self.fused:                                 # q8_1 (+ fp32 shared) GLU rows, residual, router weights in; x out
             sh_in = F // 32 * 36 if self.shared_q8 else F * 4
@@ -204,11 +214,12 @@ class MoeDecodeModel:
                                                          H, U * F, F, U, None, 0, None, 0, 0, None, 0, s),
                   "gate_up_norm q8_K")
             return
+        q8 = not self.f32_rows                         # q8_1 copies of the GLU rows
         check(lib().ggml_hip_moe_ffn_gate_up_norm(0, C.byref(ly.t_up), None, C.byref(ly.f_gu), src.data_ptr(),
                                                   self.norm[l].data_ptr(), self.eps, self.ids[l].data_ptr(),
                                                   self.h.data_ptr(), H, F, self.E, 1, U, H, U * F, F, U, None, 0,
-                                                  self.hq.data_ptr(), (U + 1) * nb, nb,
-                                                  self.hq[U:].data_ptr() if self.shared_q8 else None,
+                                                  self.hq.data_ptr() if q8 else None, (U + 1) * nb, nb,
+                                                  self.hq[U:].data_ptr() if q8 and self.shared_q8 else None,
                                                   (U + 1) * nb, s),
               "gate_up_norm")
 
@@ -224,6 +235,13 @@ class MoeDecodeModel:
                                                       src.data_ptr() if self.residual else None, dst.data_ptr(),
                                                       F, H, self.E, 1, U, (U + 1) * F, F, H, U, s),
                   "down_combine q8_K")
+            return
+        if self.f32_rows:                              # fp32 GLU rows, quantized to q8_1 by each wave
+            check(lib().ggml_hip_moe_ffn_down_combine(0, ACT_F32, C.byref(ly.t_down), C.byref(ly.f_dn),
+                                                      self.h.data_ptr(), self.ids[l].data_ptr(), self.w[l].data_ptr(),
+                                                      src.data_ptr() if self.residual else None, dst.data_ptr(),
+                                                      F, H, self.E, 1, U, (U + 1) * F, F, H, U, s),
+                  "down_combine f32 rows")
             return
         act = ACT_Q8_1 if self.shared_q8 else ACT_Q8_1 | ACT_SHARED_F32
         check(lib().ggml_hip_moe_ffn_down_combine(0, act, C.byref(ly.t_down),

@@ -483,6 +483,9 @@ def main():
     ap.add_argument("--act", choices=("q8_1", "q8_K"), default="q8_1",
                     help="fused plan: the dots' activations, q8_1 (ggml-CUDA MMVQ, the reference's path) or q8_K "
                          "(ggml-CPU MUL_MAT_ID for K-quant experts)")
+    ap.add_argument("--hand-off", choices=("q8_1", "f32"), default="q8_1",
+                    help="fused plan, q8_1 dots: the gate/up launch hands the GLU rows to the down launch as q8_1 "
+                         "blocks (default) or as fp32 rows that every down wave quantizes to q8_1")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: a 1 GiB copy (the counter calibration) and the gate/up "
                          "GEMV of every layer, then exit")
@@ -517,7 +520,7 @@ def main():
     t0 = time.perf_counter()
     fused = args.plan == "fused"
     model = md.MoeDecodeModel(torch, n_layers=args.layers, fused=fused, shared_q8=args.shared_rows == "q8_1",
-                              act=args.act if fused else "q8_1", mix=args.mix)
+                              act=args.act if fused else "q8_1", mix=args.mix, hand_off=args.hand_off)
     torch.cuda.synchronize()
     log(f"weights ready: {args.layers} layers in {time.perf_counter() - t0:.1f}s, "
         f"{torch.cuda.memory_allocated() / 2**30:.1f} GiB allocated")
@@ -571,11 +574,12 @@ def main():
     # the other activation format of the fused plan, on the same weights and routes
     modes = {}
     if fused:
-        main_act = model.act
-        for act in ("q8_1", "q8_K"):
-            if act == main_act:
+        main = (model.act, model.hand_off if model.act == "q8_1" else "f32")
+        for name, act, hand_off in (("q8_1", "q8_1", "q8_1"), ("q8_K", "q8_K", "f32"),
+                                    ("q8_1, fp32 hand-off", "q8_1", "f32")):
+            if (act, hand_off) == main:
                 continue
-            model.act = act
+            model.act, model.hand_off = act, hand_off
             model.x.copy_(x0)
             model.set_routing(ids_dev[0], w_dev[0])
             model.capture()
@@ -595,12 +599,13 @@ def main():
             ms2 = e0.elapsed_time(e1) / n2
             g2, _ = time_kernel(torch, model, gate_up_launcher(model), args.kernel_rounds)
             d2, _ = time_kernel(torch, model, down_launcher(model), args.kernel_rounds)
-            modes[act] = {"ms_per_step": round(ms2, 4), "tok_per_s": round(1000.0 / ms2, 2), "steps": n2,
+            modes[name] = {"ms_per_step": round(ms2, 4), "tok_per_s": round(1000.0 / ms2, 2), "steps": n2,
                           "gate_up_us_per_launch": round(g2 * 1000, 3), "down_us_per_launch": round(d2 * 1000, 3),
                           "gate_up_bytes_per_launch": model.gate_up_bytes(),
                           "down_bytes_per_launch": model.down_bytes()}
-            log(f"{act} activations: {ms2 * 1000:.1f} us/token, gate/up {g2 * 1000:.2f} us, down {d2 * 1000:.2f} us")
-        model.act = main_act
+            log(f"{name}: {ms2 * 1000:.1f} us/token, gate/up {g2 * 1000:.2f} us, down {d2 * 1000:.2f} us")
+        model.act = main[0]
+        model.hand_off = main[1] if main[0] == "q8_1" else args.hand_off
 
     cpu = None
     if not args.no_cpu:
@@ -630,7 +635,8 @@ def main():
                    "layers": model.L, "experts": model.E, "hidden": model.H, "ffn": model.F, "top_k": model.U,
                    "routed_type": "q2_K", "shared_type": "q4_K", "batch": 1,
                    "plan": f"{args.plan}: {2 if fused else 3} launches per layer",
-                   "shared_rows": args.shared_rows, "activations": model.act},
+                   "shared_rows": args.shared_rows, "activations": model.act,
+                   "hand_off": "fp32 rows" if model.f32_rows else "q8_1 rows"},
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "tok_per_s": round(tok_s, 2),
         "bytes_per_step": bpt,

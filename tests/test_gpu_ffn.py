@@ -243,9 +243,11 @@ def test_fused_layer_against_oracle(torch_gpu, mc, O):
     assert O.rel_l2(m.x_next.cpu().numpy(), want_x) <= 1e-5
 
 
-def test_fused_decode_equals_op_plan(torch_gpu, mc):
+@pytest.mark.parametrize("hand_off", ["q8_1", "f32"])
+def test_fused_decode_equals_op_plan(torch_gpu, mc, hand_off):
     """Three tokens through the fused plan and through the op-by-op plan: identical
-    residual streams after every token, eager and under graph replay."""
+    residual streams after every token, eager and under graph replay.  hand_off f32: the
+    gate/up launch writes only fp32 GLU rows and every down wave quantizes its row to q8_1."""
     torch = torch_gpu
     md = import_module("a6000_custom_kernels_amd.moe_decode")
     m = md.MoeDecodeModel(torch, n_layers=3, n_experts=16, hidden=1024, ffn=512, n_used=4, seed=5, fused=False)
@@ -260,6 +262,7 @@ def test_fused_decode_equals_op_plan(torch_gpu, mc):
         torch.cuda.synchronize()
         ref.append(m.x.clone())
     m.fused = True
+    m.hand_off = hand_off
     m.x.copy_(x0)
     for t in range(3):
         m.set_routing(ids_d[t], w_d[t])
