@@ -1074,6 +1074,12 @@ __device__ __forceinline__ void q8K_chunks(const float (&v)[N][4], uint8_t *cons
 // multiple, so every block is read with 128-bit LDS reads.
 constexpr int Q8K_LDS_STRIDE = 304;
 
+// Stride of the 256-value units (eight q8_1 blocks, 288 bytes) of the fused gate/up kernel's LDS
+// activation row: 16 bytes of padding per unit.  With the packed 288-byte stride the 16 units of a
+// 4096-value row lie 72 dwords apart, so their 16-byte reads by one instruction share 8 bank groups
+// of the 64 banks (a 2-way conflict); 76 dwords apart they use 16 distinct groups.
+constexpr int Q8_1_LDS_STRIDE = 304;
+
 // G blocks b0 .. b0 + G - 1 of quantize_row_lds_q8K, interleaved.
 template <int G>
 __device__ __forceinline__ void q8K_row_blocks(const float *x, uint8_t *q, int b0, bool al) {
@@ -1163,7 +1169,10 @@ __device__ __forceinline__ void rms_chunk_sums(const v4f xv[N], float out[N]) {
     for (int i = 0; i < N; ++i) out[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a[i]), 0));
 }
 
-template <int N>
+// USTRIDE: bytes from one 256-value chunk's eight q8_1 blocks to the next chunk's in y (288:
+// packed, as ggml stores the row; Q8_1_LDS_STRIDE: padded, so that 16 chunks' 16-byte LDS reads
+// fall in 16 distinct bank groups).
+template <int N, int USTRIDE = 288>
 __device__ __forceinline__ void quantize_chunks(const v4f xv[N], const v4f nwv[N], float s, uint8_t *y, const int j[N],
                                                 int16_t *s16) {
     const int lane = threadIdx.x % WAVE;
@@ -1227,8 +1236,8 @@ __device__ __forceinline__ void quantize_chunks(const v4f xv[N], const v4f nwv[N
     for (int i = 0; i < N; ++i) cs[i] += __builtin_amdgcn_update_dpp(0, cs[i], DPP_QUAD_XOR2, 0xF, 0xF, false);
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-        const int e = j[i] * RMS_CHUNK + 4 * lane;
-        uint8_t *yb = y + (e / 32) * 36;
+        const int e = 4 * lane;                          // value index within chunk j[i]
+        uint8_t *yb = y + j[i] * USTRIDE + (e / 32) * 36;
         *(u32 *) (yb + 4 + (e % 32)) = packed[i];
         *(u32 *) yb = (u32) f2h_bits(d[i]);
         s16[16 * j[i] + lane / 4] = (int16_t) cs[i];

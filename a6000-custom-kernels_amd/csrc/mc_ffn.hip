@@ -157,7 +157,7 @@ __device__ __forceinline__ void gu_prologue(const GemvArgs &a, int t, int p, flo
         }
         q8K_chunks<PC>(v, yb, yo, write_y_out);
     } else {
-        quantize_chunks<PC>(xv, nwv, scale, ys, jc, s16);
+        quantize_chunks<PC, Q8_1_LDS_STRIDE>(xv, nwv, scale, ys, jc, s16);
         if (write_y_out) {
 #pragma unroll
             for (int ci = 0; ci < PC; ++ci) {
@@ -274,11 +274,11 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
         float su, sg;
         if (sh) {
             if constexpr (TS != 0) {
-                step_dots<TS, AQ, true, AQ == ACT_Q8_K ? Q8K_LDS_STRIDE : 0>(a, s, span, ys, su, sg, s16);
+                step_dots<TS, AQ, true, AQ == ACT_Q8_K ? Q8K_LDS_STRIDE : Q8_1_LDS_STRIDE>(a, s, span, ys, su, sg, s16);
                 rl = step_store<TS>(a, s, su, sg, v);
             }
         } else {
-            step_dots<TW, AQ, true, AQ == ACT_Q8_K ? Q8K_LDS_STRIDE : 0>(a, s, span, ys, su, sg, s16);
+            step_dots<TW, AQ, true, AQ == ACT_Q8_K ? Q8K_LDS_STRIDE : Q8_1_LDS_STRIDE>(a, s, span, ys, su, sg, s16);
             rl = step_store<TW>(a, s, su, sg, v);
         }
     }
@@ -444,7 +444,7 @@ static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act, int n_cu) {
     if (a.mode == FFN_GATE_UP_NORM) {
         if (a.ncols % RMS_CHUNK || a.ncols > 8192) return hipErrorInvalidValue;
         // the normalized row: q8_1 blocks, or q8_K blocks (one per 256 values) for q8_K dots
-        const uint32_t yrow = a.dot_act == ACT_Q8_K ? (uint32_t) (a.ncols / 256 * Q8K_LDS_STRIDE) : (uint32_t) (a.ncols / 32 * 36);
+        const uint32_t yrow = (uint32_t) (a.ncols / 256) * (a.dot_act == ACT_Q8_K ? Q8K_LDS_STRIDE : Q8_1_LDS_STRIDE);
         const uint32_t common = round16(yrow) + 16u + 4u * 32u + 4u * 32u + 2u * (uint32_t) (a.ncols / 16);
         int rps, sh_rps;
         if (a.hq) {
