@@ -739,14 +739,18 @@ __device__ __forceinline__ float step_row_sum(float *red, float v, int nu) {
     return s;
 }
 
-// q8 codes roundf(v / d) of values |v| <= amax, d = amax / 127 (IEEE), with one IEEE
-// reciprocal per block instead of a division per value.  For a normal, finite d the
-// product y = v * fl(1/d) is within 2^-15 of fl(v / d): |v / d| <= 127 + 2^-16, the two
-// roundings of the product add at most 2^-16 and fl(v / d) itself at most 2^-18.  So
-// wherever y lies at least 2^-14 away from a half-integer, rint(y) == roundf(fl(v / d)).
-// The remaining values, and every value of a block whose d is zero, subnormal or not
-// finite, are flagged (slow) for the division.
+// q8 codes roundf(v / d) of values |v| <= amax, d = amax / 127 (IEEE), with one hardware
+// reciprocal per block (v_rcp_f32, relative error at most 2^-23) instead of a division per
+// value.  For a normal, finite d the product y = v * rcp(d) is within 2^-15 of fl(v / d):
+// |v / d| <= 127 (1 + 2^-24), the reciprocal's error and the product's rounding add at most
+// 1.5 * 2^-23 * 127 < 2^-15.4, and fl(v / d) itself is within 2^-17 of v / d.  So wherever y
+// lies at least 2^-14 away from a half-integer, rint(y) == roundf(fl(v / d)).  The remaining
+// values, and every value of a block whose d is zero, subnormal or not finite, are flagged
+// (slow) for the division.  (d <= FLT_MAX / 127 keeps rcp(d) a normal number.)
 __device__ __forceinline__ bool q8_scale_ok(float d) { return d >= 0x1p-126f && d <= 0x1.fffffep+127f; }
+
+// The reciprocal the shortcut multiplies by (1 when the block takes the division).
+__device__ __forceinline__ float q8_inv(float d, bool d_ok) { return __builtin_amdgcn_rcpf(d_ok ? d : 1.0f); }
 
 __device__ __forceinline__ int q8_code_fast(float v, float inv, bool d_ok, bool &slow) {
     const float y = v * (d_ok ? inv : 0.0f);
@@ -772,7 +776,7 @@ __device__ __forceinline__ int8_t q8_1_lane(float x, float &d, float &sum) {
     d = amax / 127.0f;
     const bool dok = q8_scale_ok(d);
     bool slow;
-    int q = q8_code_fast(x, 1.0f / (dok ? d : 1.0f), dok, slow);
+    int q = q8_code_fast(x, q8_inv(d, dok), dok, slow);
     if (__builtin_amdgcn_ballot_w64(slow) != 0) {            // rare: see q8_code_fast
         if (slow) q = q8_code_exact(x, d);
     }
@@ -813,7 +817,7 @@ __device__ __forceinline__ void quantize_row_lds(const float *x, uint8_t *q, int
         amax = fmaxf(amax, xor_lanes<1>(amax));              // the partner lane of the block
         const float d = amax / 127.0f;
         const bool dok = q8_scale_ok(d);
-        const float inv = 1.0f / (dok ? d : 1.0f);
+        const float inv = q8_inv(d, dok);
         int qv[16];
         u32 slow = 0u;
 #pragma unroll
@@ -955,7 +959,7 @@ __device__ __forceinline__ void quantize_chunk(const float xv[4], bool norm, flo
     }
     const float d = amax / 127.0f;
     const bool dok = q8_scale_ok(d);
-    const float inv = 1.0f / (dok ? d : 1.0f);
+    const float inv = q8_inv(d, dok);
     int q[4];
     u32 slow = 0u;
 #pragma unroll
@@ -1197,7 +1201,7 @@ __device__ __forceinline__ void quantize_chunks(const v4f xv[N], const v4f nwv[N
     for (int i = 0; i < N; ++i) {
         d[i] = amax[i] / 127.0f;
         dok[i] = q8_scale_ok(d[i]);
-        inv[i] = 1.0f / (dok[i] ? d[i] : 1.0f);
+        inv[i] = q8_inv(d[i], dok[i]);
     }
     int q[N][4];
     u32 slow = 0u;
