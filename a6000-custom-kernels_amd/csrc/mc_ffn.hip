@@ -157,7 +157,23 @@ __device__ __forceinline__ void gu_prologue(const GemvArgs &a, int t, int p, flo
         }
         q8K_chunks<PC>(v, yb, yo, write_y_out);
     } else {
-        quantize_chunks<PC, Q8_1_LDS_STRIDE>(xv, nwv, scale, ys, jc, s16);
+        // one chunk per trip of a rolled loop: the unrolled form interleaves the PC chunks'
+        // dependency chains but is PC times the code, which every dispatch fetches into a cold
+        // instruction cache (this launch alternates with the down launch); measured 0.1 us faster
+#pragma unroll 1
+        for (int ci = 0; ci < PC; ++ci) {
+            v4f x1[1] = {xv[0]}, n1[1] = {nwv[0]};
+            int j1[1] = {jc[0]};
+#pragma unroll
+            for (int k = 1; k < PC; ++k) {
+                if (ci == k) {
+                    x1[0] = xv[k];
+                    n1[0] = nwv[k];
+                    j1[0] = jc[k];
+                }
+            }
+            quantize_chunks<1, Q8_1_LDS_STRIDE>(x1, n1, scale, ys, j1, s16);
+        }
         if (write_y_out) {
 #pragma unroll
             for (int ci = 0; ci < PC; ++ci) {
