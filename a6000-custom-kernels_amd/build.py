@@ -82,6 +82,15 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+def build_single(src: Path, lib: Path, verbose: bool = False) -> Path:
+    """One self-contained HIP source (the bench's read-floor probe) as its own shared library,
+    with the library's device flags."""
+    tmp = lib.with_suffix(".so.tmp")
+    _run([HIPCC, *DEVICE_FLAGS, "-shared", "-o", tmp, src], verbose)
+    os.replace(tmp, lib)
+    return lib
+
+
 def build_hostsim(verbose: bool = False) -> Path:
     """Test-only: the same registry/step code linked against a host-memory
     simulated device (tests/native/sim_device.cpp); no kernels, no GPU."""

@@ -120,6 +120,58 @@ def traffic_probe(torch, model, md):
     log(f"traffic probe done: copy {4 * n} bytes x3, gate/up GEMV x{2 * model.L}")
 
 
+def read_floor(torch, model, md, rounds):
+    """The cost of one fused gate/up launch's bytes with nothing else in the way (bench_floor.hip): every
+    layer's GEMV steps (the same spans, routing, step list and 8-wave workgroups as the gate/up launch) only
+    streamed into LDS; the same steps in one-wave workgroups; an empty launch of the same grid.  One graph
+    of the model's layers each, timed like the kernels."""
+    import numpy as np
+    lib = C.CDLL(str(ROOT / "bench_floor.so"))
+    lib.floor_launch.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_uint, C.c_uint, C.c_void_p, C.c_void_p]
+    lib.floor_launch_empty.argtypes = [C.c_uint, C.c_uint, C.c_void_p]
+    ids_np, _ = md.make_routing(1, model.L, model.E, model.U, seed=7)
+    step_t = np.dtype([("gate", np.uint64), ("up", np.uint64), ("bytes", np.uint32), ("pad", np.uint32)])
+    F, H = model.F, model.H
+    rb, rbs = md.row_bytes(model.wtype, H), md.row_bytes(model.sh_type, H)
+    rps, sh_rps = 4, 4                                   # the q8_1 hand-off's 32-row workgroups of 8 steps
+    steps, nbytes = [], 0
+    for l, ly in enumerate(model.layers):
+        st = []
+        for r0 in range(0, F, sh_rps):
+            st.append((ly.sh_gate.data_ptr() + r0 * rbs, ly.sh_up.data_ptr() + r0 * rbs, sh_rps * rbs, 0))
+        eb = rb * F
+        for e in ids_np[0, l]:
+            for r0 in range(0, F, rps):
+                st.append((ly.gate.data_ptr() + int(e) * eb + r0 * rb, ly.up.data_ptr() + int(e) * eb + r0 * rb,
+                           rps * rb, 0))
+        a = np.array(st, dtype=step_t)
+        nbytes = int(2 * a["bytes"].astype(np.int64).sum())
+        steps.append(torch.from_numpy(a.view(np.uint8).copy()).cuda())
+    max_bytes = max(sh_rps * rbs, rps * rb)
+    region = 2 * (((max_bytes + 1024) + 1023) // 1024 * 1024)
+    out = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    n_steps = steps[0].numel() // step_t.itemsize
+    res = {"workload": f"bytes of one gate/up launch ({model.L} layers' own spans, {n_steps} GEMV steps of 4 rows, "
+                       "gate + up each): buffer->LDS DMA with the non-temporal policy, then a wait; nothing else",
+           "bytes_per_launch": nbytes}
+
+    def launch(l, wpw):
+        sp = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        rc = lib.floor_launch(steps[l].data_ptr(), n_steps, wpw, region, max_bytes, out.data_ptr(), sp)
+        assert rc == 0, f"floor_launch returned {rc}"
+
+    for wpw, key in ((8, "fused_layout"), (1, "one_wave_workgroups")):
+        ms = graph_ms(torch, [lambda l=l, w=wpw: launch(l, w) for l in range(model.L)], rounds) / model.L
+        res[key] = {"waves_per_workgroup": wpw, "workgroups": (n_steps + wpw - 1) // wpw, **_rate(nbytes, ms)}
+    grid = (n_steps + 7) // 8
+
+    def empty():
+        rc = lib.floor_launch_empty(grid, 768, C.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert rc == 0, f"floor_launch_empty returned {rc}"
+    res["empty_launch_us"] = round(graph_ms(torch, [empty] * model.L, rounds) / model.L * 1000, 3)
+    return res
+
+
 TRAFFIC_FILES = {True: "ffn_gate_up_norm_q2K_traffic.json", False: "gemv_gate_up_q2K_traffic.json"}
 KERNEL_NAMES = {True: ("mc_ffn_gate_up_kernel<q2_K, q4_K shared> (RMSNorm + q8_1 of x, gate/up + SwiGLU)",
                        "mc_ffn_down_combine_kernel<q2_K, q4_K shared, q8_1> (down + weighted combine)"),
@@ -486,6 +538,9 @@ def main():
     ap.add_argument("--hand-off", choices=("q8_1", "f32"), default="q8_1",
                     help="fused plan, q8_1 dots: the gate/up launch hands the GLU rows to the down launch as q8_1 "
                          "blocks (default) or as fp32 rows that every down wave quantizes to q8_1")
+    ap.add_argument("--read-floor", action="store_true",
+                    help="time the gate/up launch's bytes alone (bench_floor.hip: the same spans and workgroups, "
+                         "DMA only) and an empty launch, then exit")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: a 1 GiB copy (the counter calibration) and the gate/up "
                          "GEMV of every layer, then exit")
@@ -526,6 +581,9 @@ def main():
         f"{torch.cuda.memory_allocated() / 2**30:.1f} GiB allocated")
     if args.traffic_probe:
         traffic_probe(torch, model, md)
+        return
+    if args.read_floor:
+        print(json.dumps({"read_floor": read_floor(torch, model, md, args.kernel_rounds)}), flush=True)
         return
     n_tok_routes = max(64, args.warmup + args.steps)
     ids_np, w_np = md.make_routing(n_tok_routes, model.L, model.E, model.U, seed=7)
