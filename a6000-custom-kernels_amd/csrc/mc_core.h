@@ -66,6 +66,32 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, u3
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short) 0, (int) nbytes, 0x00020000);
 }
 
+// One 16-byte-per-lane buffer->LDS DMA load (1 KiB per wave) to dst, with cache policy
+// CPOL (0, or 2: nt), issued from inline assembly.  For the intrinsic form the compiler
+// places an s_waitcnt vmcnt(0) before the wave's next LDS access of any kind (it cannot
+// tell which LDS bytes the DMA writes): the first poll of an LDS counter or read of the
+// activation row after a span's DMA then waited for the whole span, so the gate dot never
+// ran while the up span landed.  The compiler does not see this form's LDS write, so every
+// reader of the DMA'd bytes waits for them itself (wait_loads_at_most, s_waitcnt vmcnt).
+// M0 (the LDS destination) is saved and restored around the load; one wait state separates
+// the M0 write from the load that reads it.
+template <int CPOL>
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t *dst, u32 voff) {
+    static_assert(CPOL == 0 || CPOL == 2, "cache policy: 0 or nt");
+    const u32 la = (u32) __builtin_amdgcn_readfirstlane((int) (u32) (uintptr_t) (__attribute__((address_space(3))) uint8_t *) dst);
+    u32 saved;
+    if constexpr (CPOL == 2)
+        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %3, 0 offen nt lds\n\ts_mov_b32 m0, %0"
+                     : "=&s"(saved)
+                     : "s"(la), "v"(voff), "s"(r)
+                     : "memory");
+    else
+        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %3, 0 offen lds\n\ts_mov_b32 m0, %0"
+                     : "=&s"(saved)
+                     : "s"(la), "v"(voff), "s"(r)
+                     : "memory");
+}
+
 __device__ __forceinline__ u32 bload(__amdgpu_buffer_rsrc_t r, u32 off) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
@@ -551,18 +577,18 @@ __device__ __forceinline__ int dma_span(const uint8_t *base, u32 base_bytes, u32
 #pragma unroll
         for (int i = 0; i < MAXR; ++i) {
             if (i < rounds) {
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * i), 16, lane_off + 1024u * i, 0, 0, MC_WEIGHT_CPOL);
+                lds_dma16<MC_WEIGHT_CPOL>(r, lds + 1024 * i, lane_off + 1024u * i);
             }
         }
     } else {
 #pragma unroll
         for (int i = 0; i < MAXR; ++i) {
             if (i < rounds - 1)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * i), 16, lane_off + 1024u * i, 0, 0, MC_WEIGHT_CPOL);
+                lds_dma16<MC_WEIGHT_CPOL>(r, lds + 1024 * i, lane_off + 1024u * i);
         }
         const u32 last = (u32) (rounds - 1);
         if (16u * (threadIdx.x % WAVE) < lead + nbytes - 1024u * last)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * last), 16, lane_off + 1024u * last, 0, 0, MC_WEIGHT_CPOL);
+            lds_dma16<MC_WEIGHT_CPOL>(r, lds + 1024 * last, lane_off + 1024u * last);
     }
     return rounds;
 }
@@ -693,7 +719,7 @@ __device__ __forceinline__ u32 dma_bytes(const uint8_t *base, u32 base_bytes, u3
     const int rounds = (int) ((lead + nbytes + 1023u) >> 10);
     const u32 lane_off = a0 + 16u * (threadIdx.x % WAVE);
     for (int i = 0; i < rounds; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *) (lds + 1024 * i), 16, lane_off + 1024u * i, 0, 0, 0);
+        lds_dma16<0>(r, lds + 1024 * i, lane_off + 1024u * i);
     return lead;
 }
 

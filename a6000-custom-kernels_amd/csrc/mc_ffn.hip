@@ -257,16 +257,27 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
         return;
     }
     const int sw = wave - NP;
-    // the first nsh_wg workgroups of a token take sh_per_wg shared steps each, the others
-    // nwaves routed steps each (whole 32-row blocks of one matrix when hq is written)
     const int bt = b % a.wg_per_tok;
-    const int nsh_wg = a.sh_per_wg > 0 ? (a.sh_tiles_per_tok + a.sh_per_wg - 1) / a.sh_per_wg : 0;
-    const bool sh_wg = bt < nsh_wg;
-    const int local0 = sh_wg ? bt * a.sh_per_wg : a.sh_tiles_per_tok + (bt - nsh_wg) * a.nwaves;
-    const int local = local0 + sw;                              // this wave's step
+    int local0 = 0, local;                                      // local: this wave's step
+    bool sh, run;
+    if (a.mixed_wg) {
+        // waves 0 .. nr-1 take this workgroup's share of the routed steps, the next ns waves its
+        // share of the shared steps; shares differ by at most one step between workgroups
+        const int G = a.wg_per_tok, NS = a.sh_tiles_per_tok, NR = a.tiles_per_tok - NS;
+        const int nr = NR / G + (bt < NR % G ? 1 : 0), ns = NS / G + (bt < NS % G ? 1 : 0);
+        sh = sw >= nr;
+        local = sh ? bt * (NS / G) + min(bt, NS % G) + (sw - nr) : NS + bt * (NR / G) + min(bt, NR % G) + sw;
+        run = sw < nr + ns && (TS != 0 || !sh);
+    } else {
+        // the first nsh_wg workgroups of a token take sh_per_wg shared steps each, the others
+        // nwaves routed steps each (whole 32-row blocks of one matrix when hq is written)
+        const int nsh_wg = a.sh_per_wg > 0 ? (a.sh_tiles_per_tok + a.sh_per_wg - 1) / a.sh_per_wg : 0;
+        sh = bt < nsh_wg;
+        local0 = sh ? bt * a.sh_per_wg : a.sh_tiles_per_tok + (bt - nsh_wg) * a.nwaves;
+        local = local0 + sw;
+        run = (sh ? sw < a.sh_per_wg && local < a.sh_tiles_per_tok : local < a.tiles_per_tok) && (TS != 0 || !sh);
+    }
     uint8_t *span = lds + (u32) sw * a.lds_wave;
-    const bool sh = sh_wg;
-    bool run = (sh_wg ? sw < a.sh_per_wg && local < a.sh_tiles_per_tok : local < a.tiles_per_tok) && (TS != 0 || !sh);
     StepCtx s;
     if (run) {
         s = sh ? step_locate(a, true, t * a.sh_tiles_per_tok + local)
@@ -298,7 +309,7 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
             rl = step_store<TW>(a, s, su, sg, v);
         }
     }
-    if (a.hq && (!sh_wg || a.hq_sh)) gu_block_q8_1(a, t, local0, sw, sh ? a.sh_rps : a.rps, run, rl, v, red + 32, sync + 3);
+    if (a.hq && (!sh || a.hq_sh)) gu_block_q8_1(a, t, local0, sw, sh ? a.sh_rps : a.rps, run, rl, v, red + 32, sync + 3);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");      // a step skipped after a timeout: its DMA has landed
 }
 
@@ -476,30 +487,29 @@ static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act, int n_cu) {
             rps = sh_rps = r;
             a.nwaves = 32 / r;
         } else {
+            // shared steps of at most a routed step's bytes (the shared matrix rows are often
+            // wider, a larger type): every wave's span is then about the same size
             rps = WAVE / nu;
-            sh_rps = ts ? WAVE / nus : 0;
+            sh_rps = 0;
+            if (ts) {
+                sh_rps = (int) ((uint32_t) rps * rb / rbs);
+                sh_rps = sh_rps < 1 ? 1 : (sh_rps > WAVE / nus ? WAVE / nus : sh_rps);
+            }
         }
         for (;;) {
             a.tiles_per_pick = (a.nrows + rps - 1) / rps;
             a.sh_tiles_per_tok = ts ? (a.nrows + sh_rps - 1) / sh_rps : 0;
             a.tiles_per_tok = a.sh_tiles_per_tok + a.n_used * a.tiles_per_pick;
             if (!a.hq) {
-                // routed steps per workgroup: about the launch's bytes per CU (one workgroup per CU,
-                // every workgroup resident at once), the shared matrix in workgroups of at most as
-                // many bytes (sh_per_wg below)
-                const double rstep = (double) rps * rb, sstep = ts ? (double) sh_rps * rbs : 1.0;
-                const double total = (double) a.n_tok * ((double) a.n_used * a.tiles_per_pick * rstep +
-                                                         (double) a.sh_tiles_per_tok * sstep);
-                int nw = (int) (total / n_cu / rstep) + 1;
-                nw = nw < 1 ? 1 : (nw > FFN_GU_MAX_WAVES ? FFN_GU_MAX_WAVES : nw);
-                for (; nw < FFN_GU_MAX_WAVES; ++nw) {
-                    int shw = ts ? (int) (nw * rstep / sstep) : 0;
-                    shw = !ts ? 0 : (shw < 1 ? 1 : (shw > nw ? nw : shw));
-                    const int wgs = a.n_tok * ((shw ? (a.sh_tiles_per_tok + shw - 1) / shw : 0) +
-                                               (a.n_used * a.tiles_per_pick + nw - 1) / nw);
-                    if (wgs <= n_cu) break;
-                }
-                a.nwaves = nw;
+                // mixed workgroups: a token's steps spread over every CU (one workgroup per CU, each
+                // with an even share of the routed steps, then of the shared steps), more
+                // workgroups when a share would exceed FFN_GU_MAX_WAVES steps
+                const int NR = a.n_used * a.tiles_per_pick, NS = a.sh_tiles_per_tok;
+                int G = n_cu / a.n_tok;
+                G = G < 1 ? 1 : G;
+                while ((NR + G - 1) / G + (NS + G - 1) / G > FFN_GU_MAX_WAVES) ++G;
+                a.wg_per_tok = G;
+                a.nwaves = (NR + G - 1) / G + (NS + G - 1) / G;
             }
             // spans sized to the 16-byte chunk the DMA writes last (+ lead-in and over-read)
             const uint32_t sr = round16((uint32_t) rps * rb + 20u);
@@ -514,17 +524,20 @@ static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act, int n_cu) {
         }
         a.rps = rps;
         a.sh_rps = sh_rps;
-        // shared-expert workgroups of about the bytes of a routed one: the shared matrix rows are
-        // often wider (a larger type), and the launch ends with its slowest workgroup.  Its q8_1
-        // blocks (hq_sh) need whole 32-row workgroups.
+        a.mixed_wg = a.hq ? 0 : 1;
         a.sh_per_wg = 0;
-        if (ts) {
-            const double rstep = (double) rps * rb, sstep = (double) sh_rps * rbs;
-            int n = (a.hq && a.hq_sh) ? a.nwaves : (int) (a.nwaves * rstep / sstep);   // at most a routed one's bytes
-            a.sh_per_wg = n < 1 ? 1 : (n > a.nwaves ? a.nwaves : n);
+        if (a.hq) {
+            // shared-expert workgroups of about the bytes of a routed one: the shared matrix rows
+            // are often wider (a larger type), and the launch ends with its slowest workgroup.
+            // Its q8_1 blocks (hq_sh) need whole 32-row workgroups.
+            if (ts) {
+                const double rstep = (double) rps * rb, sstep = (double) sh_rps * rbs;
+                int n = a.hq_sh ? a.nwaves : (int) (a.nwaves * rstep / sstep);   // at most a routed one's bytes
+                a.sh_per_wg = n < 1 ? 1 : (n > a.nwaves ? a.nwaves : n);
+            }
+            const int nsh_wg = a.sh_per_wg ? (a.sh_tiles_per_tok + a.sh_per_wg - 1) / a.sh_per_wg : 0;
+            a.wg_per_tok = nsh_wg + (a.tiles_per_tok - a.sh_tiles_per_tok + a.nwaves - 1) / a.nwaves;
         }
-        const int nsh_wg = a.sh_per_wg ? (a.sh_tiles_per_tok + a.sh_per_wg - 1) / a.sh_per_wg : 0;
-        a.wg_per_tok = nsh_wg + (a.tiles_per_tok - a.sh_tiles_per_tok + a.nwaves - 1) / a.nwaves;
         a.lds_y = (uint32_t) a.nwaves * a.lds_wave;
         a.lds_part = a.lds_y + round16(yrow);
         a.lds_total = a.lds_part + 16u + 4u * 32u + 4u * 32u + 2u * (uint32_t) (a.ncols / 16);

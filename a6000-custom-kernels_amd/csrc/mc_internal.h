@@ -134,9 +134,12 @@ struct GemvArgs {
     int32_t mode;
     int32_t nwaves;               // step waves per workgroup (FFN_GATE_UP_NORM: plus FFN_GU_PRO_WAVES)
     int32_t dot_act;              // fused kernels: the dots' activation format (ACT_Q8_1 or ACT_Q8_K)
-    int32_t sh_per_wg;            // FFN_GATE_UP_NORM: steps of a shared-expert workgroup (its first
-                                  //   workgroups take only shared steps, about as many bytes as the
-                                  //   routed workgroups' nwaves steps)
+    int32_t sh_per_wg;            // FFN_GATE_UP_NORM with hq: steps of a shared-expert workgroup (its
+                                  //   first workgroups take only shared steps, about as many bytes as
+                                  //   the routed workgroups' nwaves steps)
+    int32_t mixed_wg;             // FFN_GATE_UP_NORM without hq: each of a token's wg_per_tok
+                                  //   workgroups takes an even share of the routed steps, then of the
+                                  //   shared steps (shares differ by at most one step)
     int32_t wg_per_tok;           // workgroups per token
     int32_t tiles_per_tok;        // steps per token: shared tiles first, then the routed picks'
     uint32_t lds_wave;            // LDS bytes of one wave's region (spans, activation staging)
