@@ -74,11 +74,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, u3
 // ran while the up span landed.  The compiler does not see this form's LDS write, so every
 // reader of the DMA'd bytes waits for them itself (wait_loads_at_most, s_waitcnt vmcnt).
 // M0 (the LDS destination) is saved and restored around the load; one wait state separates
-// the M0 write from the load that reads it.
+// the M0 write from the load that reads it.  dst is a generic pointer into LDS, whose low 32
+// bits are the LDS address (an address-space cast would add a null check per load).
 template <int CPOL>
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t *dst, u32 voff) {
     static_assert(CPOL == 0 || CPOL == 2, "cache policy: 0 or nt");
-    const u32 la = (u32) __builtin_amdgcn_readfirstlane((int) (u32) (uintptr_t) (__attribute__((address_space(3))) uint8_t *) dst);
+    const u32 la = (u32) __builtin_amdgcn_readfirstlane((int) (u32) (uintptr_t) dst);
     u32 saved;
     if constexpr (CPOL == 2)
         asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %3, 0 offen nt lds\n\ts_mov_b32 m0, %0"
