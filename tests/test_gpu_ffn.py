@@ -41,9 +41,11 @@ def _norm_q8_1(torch, mc, x, nw, eps):
     ("Q3_K", None, 1024, 128, 1, True, False, True),
     ("Q6_K", "Q5_K", 1024, 64, 2, True, True, True),
     ("Q5_K", "Q2_K", 768, 200, 1, True, False, True),
-    # rows longer than 16 chunks: eight chunks per prologue wave
+    # rows longer than 16 chunks: eight chunks per prologue wave (no q8_1 copies: mixed workgroups,
+    # each an even share of a token's routed and shared steps)
     ("Q2_K", "Q4_K", 6144, 96, 2, True, True, True),
     ("Q4_K", "Q2_K", 8192, 64, 1, False, False, True),
+    ("Q2_K", "Q4_K", 6144, 200, 3, True, True, True),
     # routed q8_1 copies without the shared one: shared-expert workgroups sized by bytes
     ("Q2_K", "Q4_K", 4096, 768, 1, True, False, False),
     ("Q2_K", "Q6_K", 2048, 96, 3, True, True, False),
