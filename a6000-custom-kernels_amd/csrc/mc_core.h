@@ -530,6 +530,7 @@ __device__ __forceinline__ float silu_f(float x) {
 }
 
 __device__ __forceinline__ float glu_apply(int op, float g, float up, float limit) {
+#pragma clang fp contract(off)          // every caller rounds each step alike (GEGLU's 1 + c * g * g)
     switch (op) {
         case 0: return up * (g > 0.0f ? g : 0.0f);                                                   // REGLU
         case 1: return up * (0.5f * g * (1.0f + tanhf(0.79788456080286535587989211986876f * g * (1.0f + 0.044715f * g * g)))); // GEGLU
