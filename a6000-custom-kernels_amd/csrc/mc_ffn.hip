@@ -40,6 +40,8 @@
 
 namespace mc {
 
+__device__ __forceinline__ int lane_of() { return (int) (threadIdx.x % WAVE); }
+
 // ---------------------------------------------------------------------------
 // device status word
 // ---------------------------------------------------------------------------
@@ -225,7 +227,7 @@ __device__ __forceinline__ void gu_block_q8_1(const GemvArgs &a, int t, int loca
 // each).  The step waves issue their weight spans first and only wait for the
 // normalized row once their gate span has landed; no workgroup barrier follows the
 // start, so no wave waits for another wave's weight stream.
-// Dynamic LDS: [nwaves x (up span | gate span)] [q8_1 row] [4 counters | 32 chunk sums | 32-row block |
+// Dynamic LDS: [nwaves x (up span | gate span)] [q8_1 row] [5 counters (32 bytes) | 32 chunk sums | 32-row block |
 // 16-value sums of the row (int16)]
 template <int TW, int TS, int AQ>
 __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void mc_ffn_gate_up_kernel(const GemvArgs a) {
@@ -241,13 +243,14 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
     const int t = b / a.wg_per_tok;
     uint8_t *ys = lds + a.lds_y;
     u32 *sync = (u32 *) (lds + a.lds_part);
-    float *red = (float *) (lds + a.lds_part + 16);
-    int16_t *s16 = (int16_t *) (lds + a.lds_part + 16 + 4 * 32 + 4 * 32);   // 16-value sums of y
+    float *red = (float *) (lds + a.lds_part + 32);
+    int16_t *s16 = (int16_t *) (lds + a.lds_part + 32 + 4 * 32 + 4 * 32);   // 16-value sums of y
     if (threadIdx.x == 0) {
         sync[0] = 0u;
         sync[1] = 0u;
         sync[2] = 0u;
         sync[3] = 0u;
+        sync[4] = 0u;
     }
     lds_barrier();                                            // counters set; nothing is in flight yet
     if (wave < NP) {
@@ -277,6 +280,11 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
         local = local0 + sw;
         run = (sh ? sw < a.sh_per_wg && local < a.sh_tiles_per_tok : local < a.tiles_per_tok) && (TS != 0 || !sh);
     }
+    // the first n_early step waves (one per SIMD) issue their spans before the others, so their
+    // bytes land early in the stream and their dots overlap the rest of it (0.1-0.2 us off a
+    // launch of mixed workgroups; no change in workgroups of 32-row blocks)
+    const int n_early = a.nwaves / 2;
+    const bool early = sw < n_early, late = n_early > 0 && !early;
     uint8_t *span = lds + (u32) sw * a.lds_wave;
     StepCtx s;
     if (run) {
@@ -287,13 +295,17 @@ __global__ __launch_bounds__((FFN_GU_MAX_WAVES + FFN_GU_PRO_WAVES) *WAVE) void m
     }
     if (run) {
         wait_lds_count(a, sync + 2, (u32) NP);                // the prologue's loads go out first
+        if (late) wait_lds_count(a, sync + 4, (u32) n_early);   // then the early waves' spans
         if (sh) {
             if constexpr (TS != 0) step_dma<TS, true>(a, s, span);
         } else {
             step_dma<TW, true>(a, s, span);
         }
+        if (early && lane_of() == 0) __hip_atomic_fetch_add(sync + 4, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         wait_loads_at_most(s.wgate ? s.n_up : 0);             // gate span landed (up may still land)
         run = wait_lds_count(a, sync + 1, (u32) NP);          // the normalized row is complete
+    } else if (early && lane_of() == 0) {
+        __hip_atomic_fetch_add(sync + 4, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
     float v = 0.0f;
     int rl = -1;
@@ -472,7 +484,7 @@ static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act, int n_cu) {
         if (a.ncols % RMS_CHUNK || a.ncols > 8192) return hipErrorInvalidValue;
         // the normalized row: q8_1 blocks, or q8_K blocks (one per 256 values) for q8_K dots
         const uint32_t yrow = (uint32_t) (a.ncols / 256) * (a.dot_act == ACT_Q8_K ? Q8K_LDS_STRIDE : Q8_1_LDS_STRIDE);
-        const uint32_t common = round16(yrow) + 16u + 4u * 32u + 4u * 32u + 2u * (uint32_t) (a.ncols / 16);
+        const uint32_t common = round16(yrow) + 32u + 4u * 32u + 4u * 32u + 2u * (uint32_t) (a.ncols / 16);
         int rps, sh_rps;
         if (a.hq) {
             // workgroups of exactly one q8_1 block of rows: steps of a power-of-two row count
@@ -540,7 +552,7 @@ static hipError_t ffn_layout(GemvArgs &a, int tw, int ts, int act, int n_cu) {
         }
         a.lds_y = (uint32_t) a.nwaves * a.lds_wave;
         a.lds_part = a.lds_y + round16(yrow);
-        a.lds_total = a.lds_part + 16u + 4u * 32u + 4u * 32u + 2u * (uint32_t) (a.ncols / 16);
+        a.lds_total = a.lds_part + 32u + 4u * 32u + 4u * 32u + 2u * (uint32_t) (a.ncols / 16);
         a.n_tiles = a.tiles_per_tok * a.n_tok;
         return hipSuccess;
     }
