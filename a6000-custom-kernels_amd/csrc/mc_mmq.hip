@@ -212,21 +212,49 @@ struct MmqTile {
     static_assert(MMQ_ROWS * RP % (WAVE * DB) == 0, "whole DMA instructions per tile");
 };
 
-// Issues the DMA of super-block s: MMQ_ROWS weight rows (one super-block, or its
-// window, each; rows row_bytes apart in memory, back to back in LDS) and nb
-// activation records.
+// Per-lane byte offsets of the wave's weight-tile DMA instructions (instruction
+// wave + MMQ_WAVES k), without the super-block term s * SBB: they depend only on the
+// workgroup's rows, so they are computed once, not per stage.  Piece q of the tile is
+// part q % CH of row q / CH.  Windowed types keep the row start and the part apart
+// (the window start is rounded down to its dword after adding s * SBB).
 template <int T>
-__device__ __forceinline__ void mmq_issue(const MmqArgs &a, const uint8_t *wbase, int row0, int s, int blk0, int nb,
-                                          uint8_t *wl, uint8_t *rl) {
+struct MmqLanes {
+    static constexpr int K = (MmqTile<T>::N_INS + MMQ_WAVES - 1) / MMQ_WAVES;
+    uint32_t row[K];            // b0 + (row0 + q / CH) * row_bytes (plain types: + DB * (q % CH))
+    uint32_t part[K];           // DB * (q % CH) (windowed types only)
+};
+
+template <int T>
+__device__ __forceinline__ void mmq_lanes(const MmqArgs &a, const uint8_t *wbase, int row0, int wave, MmqLanes<T> &L) {
     using G = MmqTile<T>;
-    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    const int lane = threadIdx.x % WAVE;
     const uint32_t row_bytes = (uint32_t) (a.ncols / 256) * G::SBB;
     const uint32_t b0 = (uint32_t) ((uintptr_t) wbase & 3u);     // 0 except for a 2-byte aligned Q6_K expert
+#pragma unroll
+    for (int k = 0; k < MmqLanes<T>::K; ++k) {
+        const int q = (wave + MMQ_WAVES * k) * WAVE + lane;
+        const uint32_t part = (uint32_t) G::DB * (uint32_t) (q % G::CH);
+        L.row[k] = b0 + (uint32_t) (row0 + q / G::CH) * row_bytes + (G::WIN ? 0u : part);
+        L.part[k] = part;
+    }
+}
+
+// Issues the DMA of super-block s: MMQ_ROWS weight rows (one super-block, or its
+// window, each; rows row_bytes apart in memory, back to back in LDS) and nb
+// activation records.  wave is the wave's index, uniform across the wave.
+template <int T>
+__device__ __forceinline__ void mmq_issue(const MmqArgs &a, const uint8_t *wbase, const MmqLanes<T> &L, int wave, int s,
+                                          int blk0, int nb, uint8_t *wl, uint8_t *rl) {
+    using G = MmqTile<T>;
+    const int lane = threadIdx.x % WAVE;
+    const uint32_t b0 = (uint32_t) ((uintptr_t) wbase & 3u);
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(wbase - b0, (uint32_t) a.expert_bytes + b0);
-    for (int i = wave; i < G::N_INS; i += MMQ_WAVES) {
-        const int q = i * WAVE + lane;                       // piece q of the tile: row q / CH, part q % CH
-        const uint32_t o = b0 + (uint32_t) (row0 + q / G::CH) * row_bytes + (uint32_t) s * G::SBB;
-        const uint32_t off = (G::WIN ? (o & ~3u) : o) + (uint32_t) G::DB * (uint32_t) (q % G::CH);
+    const uint32_t so = (uint32_t) s * G::SBB;
+#pragma unroll
+    for (int k = 0; k < MmqLanes<T>::K; ++k) {
+        const int i = wave + MMQ_WAVES * k;
+        if (i >= G::N_INS) break;
+        const uint32_t off = G::WIN ? ((L.row[k] + so) & ~3u) + L.part[k] : L.row[k] + so;
         lds_void_t *dst = (lds_void_t *) (wl + WAVE * G::DB * i);
         if constexpr (G::DB == 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, dst, 16, off, 0, 0, 0);
         else __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, dst, 4, off, 0, 0, 0);
@@ -579,7 +607,8 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int N_INS = MmqTile<T>::N_INS;
     constexpr uint32_t WT = MmqTile<T>::WT;                 // weight tile bytes per matrix and super-block
-    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    // the wave index is uniform across the wave: keep it (and the loops over it) scalar
+    const int lane = threadIdx.x % WAVE, wave = __builtin_amdgcn_readfirstlane((int) (threadIdx.x / WAVE));
     const int e = blockIdx.y;
     const int *blk_off = (const int *) (a.ws + a.ws_blk_off);
     const int blk_first = blk_off[e], nblk = blk_off[e + 1] - blk_first;
@@ -592,6 +621,8 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
     const uint32_t stage = (GATE ? 2u : 1u) * WT + MAXB * MMQ_REC_BYTES + 1024u;
     const int *blk_tab = (const int *) (a.ws + a.ws_blk_tab);
     const int *list = (const int *) (a.ws + a.ws_list);
+    MmqLanes<T> lanes;                                      // the gate's DMA has the same offsets
+    mmq_lanes<T>(a, wup, row0, wave, lanes);
 
     for (int g0 = 0; g0 < nblk; g0 += MAXB) {
         const int nb = min(MAXB, nblk - g0);
@@ -603,8 +634,8 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
         const int per_stage = mmq_issue_count(nb, wave, N_INS) + (GATE ? mmq_issue_count(0, wave, N_INS) : 0);
         auto issue = [&](int s) {
             uint8_t *st = lds + (uint32_t) (s & 1) * stage;
-            mmq_issue<T>(a, wup, row0, s, blk_first + g0, nb, st, st + (GATE ? 2 : 1) * WT);
-            if (GATE) mmq_issue<T>(a, wgt, row0, s, blk_first + g0, 0, st + WT, nullptr);
+            mmq_issue<T>(a, wup, lanes, wave, s, blk_first + g0, nb, st, st + (GATE ? 2 : 1) * WT);
+            if (GATE) mmq_issue<T>(a, wgt, lanes, wave, s, blk_first + g0, 0, st + WT, nullptr);
         };
         issue(0);
         for (int s = 0; s < n_sb; ++s) {
