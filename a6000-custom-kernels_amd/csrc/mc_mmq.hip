@@ -19,8 +19,9 @@
 //   2. mc_mmq_pack_kernel: per (super-block, column block) one record holding the
 //      MFMA A fragments of the 16 pairs' activation codes, their q8_K scales and
 //      32-value sums (zeros for empty columns).
-//   3. mc_mmq_gemm_kernel<T, GATE>: one workgroup per (64 weight rows, expert);
-//      per super-block it DMAs the 64 rows' weight blocks and the records of up
+//   3. mc_mmq_gemm_kernel<T, GATE>: one workgroup per (64 weight rows with a fused gate,
+//      else 128, expert);
+//      per super-block it DMAs the rows' weight blocks and the records of up
 //      to MAXB column blocks into LDS (double-buffered), each wave
 //      multiplies 16 weight rows against them, and the epilogue applies the GLU
 //      (when a gate matrix is fused) and scatters to dst[token][slot][row].
@@ -199,60 +200,61 @@ __global__ __launch_bounds__(256) void mc_mmq_pack_kernel(const MmqArgs a) {
 //   extra two bytes belong to a neighbouring super-block (or read as zeros past
 //   the buffer) and are never used.  (Buffer->LDS DMA of 1- or 2-byte pieces writes
 //   one dword per lane, so it cannot pack 2-byte aligned rows.)
-template <int T>
+template <int T, int NW = MMQ_WAVES>
 struct MmqTile {
+    static constexpr int ROWS = 16 * NW;                                // weight rows per workgroup
     static constexpr int SBB = type_geom(T).block_bytes;
     static constexpr bool WIN = SBB % 4 != 0;
     static constexpr int DB = SBB % 16 == 0 ? 16 : 4;                  // bytes per lane and DMA
     static constexpr int RP = WIN ? SBB + 2 : SBB;                      // LDS row pitch
     static constexpr int CH = RP / DB;                                  // pieces per row
-    static constexpr int N_INS = MMQ_ROWS * RP / (WAVE * DB);           // wave DMA instructions per tile
-    static constexpr uint32_t WT = MMQ_ROWS * RP;                       // LDS tile bytes
+    static constexpr int N_INS = ROWS * RP / (WAVE * DB);               // wave DMA instructions per tile
+    static constexpr uint32_t WT = ROWS * RP;                           // LDS tile bytes
     static_assert(!WIN || SBB % 4 == 2, "windows cover super-blocks that are 2-byte aligned");
-    static_assert(MMQ_ROWS * RP % (WAVE * DB) == 0, "whole DMA instructions per tile");
+    static_assert(ROWS * RP % (WAVE * DB) == 0, "whole DMA instructions per tile");
 };
 
 // Per-lane byte offsets of the wave's weight-tile DMA instructions (instruction
-// wave + MMQ_WAVES k), without the super-block term s * SBB: they depend only on the
+// wave + NW k), without the super-block term s * SBB: they depend only on the
 // workgroup's rows, so they are computed once, not per stage.  Piece q of the tile is
 // part q % CH of row q / CH.  Windowed types keep the row start and the part apart
 // (the window start is rounded down to its dword after adding s * SBB).
-template <int T>
+template <int T, int NW>
 struct MmqLanes {
-    static constexpr int K = (MmqTile<T>::N_INS + MMQ_WAVES - 1) / MMQ_WAVES;
+    static constexpr int K = (MmqTile<T, NW>::N_INS + NW - 1) / NW;
     uint32_t row[K];            // b0 + (row0 + q / CH) * row_bytes (plain types: + DB * (q % CH))
     uint32_t part[K];           // DB * (q % CH) (windowed types only)
 };
 
-template <int T>
-__device__ __forceinline__ void mmq_lanes(const MmqArgs &a, const uint8_t *wbase, int row0, int wave, MmqLanes<T> &L) {
-    using G = MmqTile<T>;
+template <int T, int NW>
+__device__ __forceinline__ void mmq_lanes(const MmqArgs &a, const uint8_t *wbase, int row0, int wave, MmqLanes<T, NW> &L) {
+    using G = MmqTile<T, NW>;
     const int lane = threadIdx.x % WAVE;
     const uint32_t row_bytes = (uint32_t) (a.ncols / 256) * G::SBB;
     const uint32_t b0 = (uint32_t) ((uintptr_t) wbase & 3u);     // 0 except for a 2-byte aligned Q6_K expert
 #pragma unroll
-    for (int k = 0; k < MmqLanes<T>::K; ++k) {
-        const int q = (wave + MMQ_WAVES * k) * WAVE + lane;
+    for (int k = 0; k < MmqLanes<T, NW>::K; ++k) {
+        const int q = (wave + NW * k) * WAVE + lane;
         const uint32_t part = (uint32_t) G::DB * (uint32_t) (q % G::CH);
         L.row[k] = b0 + (uint32_t) (row0 + q / G::CH) * row_bytes + (G::WIN ? 0u : part);
         L.part[k] = part;
     }
 }
 
-// Issues the DMA of super-block s: MMQ_ROWS weight rows (one super-block, or its
+// Issues the DMA of super-block s: 16 NW weight rows (one super-block, or its
 // window, each; rows row_bytes apart in memory, back to back in LDS) and nb
 // activation records.  wave is the wave's index, uniform across the wave.
-template <int T>
-__device__ __forceinline__ void mmq_issue(const MmqArgs &a, const uint8_t *wbase, const MmqLanes<T> &L, int wave, int s,
+template <int T, int NW>
+__device__ __forceinline__ void mmq_issue(const MmqArgs &a, const uint8_t *wbase, const MmqLanes<T, NW> &L, int wave, int s,
                                           int blk0, int nb, uint8_t *wl, uint8_t *rl) {
-    using G = MmqTile<T>;
+    using G = MmqTile<T, NW>;
     const int lane = threadIdx.x % WAVE;
     const uint32_t b0 = (uint32_t) ((uintptr_t) wbase & 3u);
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(wbase - b0, (uint32_t) a.expert_bytes + b0);
     const uint32_t so = (uint32_t) s * G::SBB;
 #pragma unroll
-    for (int k = 0; k < MmqLanes<T>::K; ++k) {
-        const int i = wave + MMQ_WAVES * k;
+    for (int k = 0; k < MmqLanes<T, NW>::K; ++k) {
+        const int i = wave + NW * k;
         if (i >= G::N_INS) break;
         const uint32_t off = G::WIN ? ((L.row[k] + so) & ~3u) + L.part[k] : L.row[k] + so;
         lds_void_t *dst = (lds_void_t *) (wl + WAVE * G::DB * i);
@@ -263,14 +265,15 @@ __device__ __forceinline__ void mmq_issue(const MmqArgs &a, const uint8_t *wbase
     const uint8_t *recs = a.ws + a.ws_packed + ((int64_t) s * a.max_blocks + blk0) * MMQ_REC_BYTES;
     const __amdgpu_buffer_rsrc_t rr = make_rsrc(recs, (uint32_t) nb * MMQ_REC_BYTES);
     const int rounds = (nb * MMQ_REC_BYTES + 1023) / 1024;
-    for (int i = wave; i < rounds; i += MMQ_WAVES)
+    for (int i = wave; i < rounds; i += NW)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void_t *) (rl + 1024 * i), 16, 1024u * i + 16u * lane, 0, 0, 0);
 }
 
+template <int NW>
 __device__ __forceinline__ int mmq_issue_count(int nb, int wave, int n_ins) {
     int n = 0;
-    for (int i = wave; i < n_ins; i += MMQ_WAVES) ++n;
-    for (int i = wave; i < (nb * MMQ_REC_BYTES + 1023) / 1024; i += MMQ_WAVES) ++n;
+    for (int i = wave; i < n_ins; i += NW) ++n;
+    for (int i = wave; i < (nb * MMQ_REC_BYTES + 1023) / 1024; i += NW) ++n;
     return n;
 }
 
@@ -603,17 +606,19 @@ __device__ __forceinline__ void mmq_superblock_g16(const uint8_t *wrow_up, const
 }
 
 template <int T, bool GATE, int MAXB>
-__global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const MmqArgs a) {
+__global__ __launch_bounds__(mmq_waves(GATE) * WAVE) void mc_mmq_gemm_kernel(const MmqArgs a) {
+    constexpr int NW = mmq_waves(GATE);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    constexpr int N_INS = MmqTile<T>::N_INS;
-    constexpr uint32_t WT = MmqTile<T>::WT;                 // weight tile bytes per matrix and super-block
+    using G = MmqTile<T, NW>;
+    constexpr int N_INS = G::N_INS;
+    constexpr uint32_t WT = G::WT;                          // weight tile bytes per matrix and super-block
     // the wave index is uniform across the wave: keep it (and the loops over it) scalar
     const int lane = threadIdx.x % WAVE, wave = __builtin_amdgcn_readfirstlane((int) (threadIdx.x / WAVE));
     const int e = blockIdx.y;
     const int *blk_off = (const int *) (a.ws + a.ws_blk_off);
     const int blk_first = blk_off[e], nblk = blk_off[e + 1] - blk_first;
     if (nblk <= 0) return;
-    const int row0 = blockIdx.x * MMQ_ROWS;
+    const int row0 = blockIdx.x * G::ROWS;
     const int n_sb = a.ncols / 256;
     const uint8_t *wup = a.w + (int64_t) e * a.expert_bytes;
     const uint8_t *wgt = GATE ? a.w_gate + (int64_t) e * a.expert_bytes : nullptr;
@@ -621,8 +626,8 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
     const uint32_t stage = (GATE ? 2u : 1u) * WT + MAXB * MMQ_REC_BYTES + 1024u;
     const int *blk_tab = (const int *) (a.ws + a.ws_blk_tab);
     const int *list = (const int *) (a.ws + a.ws_list);
-    MmqLanes<T> lanes;                                      // the gate's DMA has the same offsets
-    mmq_lanes<T>(a, wup, row0, wave, lanes);
+    MmqLanes<T, NW> lanes;                                  // the gate's DMA has the same offsets
+    mmq_lanes<T, NW>(a, wup, row0, wave, lanes);
 
     for (int g0 = 0; g0 < nblk; g0 += MAXB) {
         const int nb = min(MAXB, nblk - g0);
@@ -631,11 +636,11 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
         for (int b = 0; b < MAXB; ++b)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[b][i] = accg[b][i] = 0.0f;
-        const int per_stage = mmq_issue_count(nb, wave, N_INS) + (GATE ? mmq_issue_count(0, wave, N_INS) : 0);
+        const int per_stage = mmq_issue_count<NW>(nb, wave, N_INS) + (GATE ? mmq_issue_count<NW>(0, wave, N_INS) : 0);
         auto issue = [&](int s) {
             uint8_t *st = lds + (uint32_t) (s & 1) * stage;
-            mmq_issue<T>(a, wup, lanes, wave, s, blk_first + g0, nb, st, st + (GATE ? 2 : 1) * WT);
-            if (GATE) mmq_issue<T>(a, wgt, lanes, wave, s, blk_first + g0, 0, st + WT, nullptr);
+            mmq_issue<T, NW>(a, wup, lanes, wave, s, blk_first + g0, nb, st, st + (GATE ? 2 : 1) * WT);
+            if (GATE) mmq_issue<T, NW>(a, wgt, lanes, wave, s, blk_first + g0, 0, st + WT, nullptr);
         };
         issue(0);
         for (int s = 0; s < n_sb; ++s) {
@@ -648,18 +653,18 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
             lds_barrier();                                    // ... and for every wave (stage s + 1 stays in flight)
             const uint8_t *st = lds + (uint32_t) (s & 1) * stage;
             const uint8_t *recs = st + (GATE ? 2 : 1) * WT;
-            const uint32_t roff = (uint32_t) (16 * wave + lane % 16) * MmqTile<T>::RP;
+            const uint32_t roff = (uint32_t) (16 * wave + lane % 16) * G::RP;
             if constexpr (T == T_Q2_K) mmq_superblock_q2K<GATE, MAXB>(st + roff, st + WT + roff, recs, nb, acc, accg);
-            else if constexpr (MmqTile<T>::WIN) {
+            else if constexpr (G::WIN) {
                 // where this row's super-block starts in its window: the same address
                 // arithmetic as mmq_issue (both matrices of an expert share it when the
                 // gate's base has the up's alignment, which the entry point checks)
                 const int wrow = row0 + 16 * wave + lane % 16;
                 const uint32_t b0 = (uint32_t) ((uintptr_t) wup & 3u);
-                const uint32_t rel = (uint32_t) wrow * (uint32_t) (n_sb * MmqTile<T>::SBB) + (uint32_t) s * MmqTile<T>::SBB;
+                const uint32_t rel = (uint32_t) wrow * (uint32_t) (n_sb * G::SBB) + (uint32_t) s * G::SBB;
                 const uint32_t sh = (b0 + rel) & 3u;
                 // rows past nrows (the last tile's padding) are never stored and never read from memory
-                const bool tail = wrow < a.nrows && sh == 0 && rel + MmqTile<T>::RP > (uint32_t) a.expert_bytes;
+                const bool tail = wrow < a.nrows && sh == 0 && rel + G::RP > (uint32_t) a.expert_bytes;
                 mmq_superblock_g16<T, GATE, MAXB>(st + roff, st + WT + roff, sh, tail, wup + rel,
                                                   GATE ? wgt + rel : nullptr, recs, nb, acc, accg);
             }
@@ -693,19 +698,21 @@ __global__ __launch_bounds__(MMQ_WAVES * WAVE) void mc_mmq_gemm_kernel(const Mmq
 
 template <int T, int MAXB>
 static hipError_t launch_mmq_tb(const MmqArgs &a, hipStream_t s) {
-    constexpr uint32_t WT = MmqTile<T>::WT;
+    using GG = MmqTile<T, mmq_waves(true)>;
+    using GP = MmqTile<T, mmq_waves(false)>;
     const bool gate = a.w_gate != nullptr;
-    const uint32_t stage = (gate ? 2u : 1u) * WT + MAXB * MMQ_REC_BYTES + 1024u;
-    const dim3 grid((unsigned) ((a.nrows + MMQ_ROWS - 1) / MMQ_ROWS), (unsigned) a.n_experts);
+    const uint32_t stage = gate ? 2u * GG::WT + MAXB * MMQ_REC_BYTES + 1024u : GP::WT + MAXB * MMQ_REC_BYTES + 1024u;
+    const int rows = gate ? GG::ROWS : GP::ROWS;
+    const dim3 grid((unsigned) ((a.nrows + rows - 1) / rows), (unsigned) a.n_experts);
     // more than the default 64 KiB of dynamic LDS: raise the kernel's limit once
     static const hipError_t attr_gate = hipFuncSetAttribute((const void *) mc_mmq_gemm_kernel<T, true, MAXB>,
-        hipFuncAttributeMaxDynamicSharedMemorySize, (int) (2 * (2 * WT + MAXB * MMQ_REC_BYTES + 1024u)));
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int) (2 * (2 * GG::WT + MAXB * MMQ_REC_BYTES + 1024u)));
     static const hipError_t attr_plain = hipFuncSetAttribute((const void *) mc_mmq_gemm_kernel<T, false, MAXB>,
-        hipFuncAttributeMaxDynamicSharedMemorySize, (int) (2 * (WT + MAXB * MMQ_REC_BYTES + 1024u)));
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int) (2 * (GP::WT + MAXB * MMQ_REC_BYTES + 1024u)));
     if (attr_gate != hipSuccess) return attr_gate;
     if (attr_plain != hipSuccess) return attr_plain;
-    if (gate) hipLaunchKernelGGL((mc_mmq_gemm_kernel<T, true, MAXB>), grid, dim3(MMQ_WAVES * WAVE), 2 * stage, s, a);
-    else hipLaunchKernelGGL((mc_mmq_gemm_kernel<T, false, MAXB>), grid, dim3(MMQ_WAVES * WAVE), 2 * stage, s, a);
+    if (gate) hipLaunchKernelGGL((mc_mmq_gemm_kernel<T, true, MAXB>), grid, dim3(mmq_waves(true) * WAVE), 2 * stage, s, a);
+    else hipLaunchKernelGGL((mc_mmq_gemm_kernel<T, false, MAXB>), grid, dim3(mmq_waves(false) * WAVE), 2 * stage, s, a);
     return hipGetLastError();
 }
 
