@@ -253,12 +253,13 @@ constexpr int RMS_CHUNK = 256;
 // ---------------------------------------------------------------------------
 
 constexpr int MMQ_COLS = 16;              // (token, slot) pairs per column block: the MFMA M dimension
-constexpr int MMQ_WAVES = 4;              // waves per GEMM workgroup with a fused gate, 16 weight rows each
-constexpr int MMQ_WAVES_PLAIN = 8;        // ... without one (half the LDS per row, so twice the rows)
-// Waves per grouped-GEMM workgroup.  A plain projection's workgroup (down: K = 768, three
-// super-blocks) takes 128 rows, so each expert's activation records are staged for half
-// as many workgroups.
-constexpr int mmq_waves(bool gate) { return gate ? MMQ_WAVES : MMQ_WAVES_PLAIN; }
+constexpr int MMQ_WAVES = 4;              // waves per GEMM workgroup, 16 weight rows each
+constexpr int MMQ_WAVES_PLAIN = 8;        // ... without a fused gate and one column block per pass
+// Waves per grouped-GEMM workgroup.  A plain projection's workgroup that takes one
+// column block per pass (down at prefill: K = 768, three super-blocks) takes 128 rows, so
+// each expert's activation records are staged for half as many workgroups; with four
+// column blocks per pass the 8-wave form needs more than 256 VGPRs (Q3_K, Q6_K).
+constexpr int mmq_waves(bool gate, int maxb) { return !gate && maxb == 1 ? MMQ_WAVES_PLAIN : MMQ_WAVES; }
 // Column blocks multiplied per pass over an expert's weights: 1 when the experts
 // average at most MMQ_FEW_PAIRS pairs (most need one block, and the smaller LDS
 // stages let more workgroups keep weight DMA in flight), else up to 4 (fewer

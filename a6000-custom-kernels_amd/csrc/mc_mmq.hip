@@ -19,8 +19,8 @@
 //   2. mc_mmq_pack_kernel: per (super-block, column block) one record holding the
 //      MFMA A fragments of the 16 pairs' activation codes, their q8_K scales and
 //      32-value sums (zeros for empty columns).
-//   3. mc_mmq_gemm_kernel<T, GATE>: one workgroup per (64 weight rows with a fused gate,
-//      else 128, expert);
+//   3. mc_mmq_gemm_kernel<T, GATE>: one workgroup per (64 weight rows, or 128 without a
+//      fused gate and with one column block per pass; expert);
 //      per super-block it DMAs the rows' weight blocks and the records of up
 //      to MAXB column blocks into LDS (double-buffered), each wave
 //      multiplies 16 weight rows against them, and the epilogue applies the GLU
@@ -217,27 +217,26 @@ struct MmqTile {
 // Per-lane byte offsets of the wave's weight-tile DMA instructions (instruction
 // wave + NW k), without the super-block term s * SBB: they depend only on the
 // workgroup's rows, so they are computed once, not per stage.  Piece q of the tile is
-// part q % CH of row q / CH.  Windowed types keep the row start and the part apart
-// (the window start is rounded down to its dword after adding s * SBB).
+// part q % CH of row q / CH.  A windowed type's window starts at the dword below its
+// super-block; as the part offset DB (q % CH) is a multiple of 4, that rounding can be
+// applied to the sum (row start + part + s * SBB).
 template <int T, int NW>
 struct MmqLanes {
     static constexpr int K = (MmqTile<T, NW>::N_INS + NW - 1) / NW;
-    uint32_t row[K];            // b0 + (row0 + q / CH) * row_bytes (plain types: + DB * (q % CH))
-    uint32_t part[K];           // DB * (q % CH) (windowed types only)
+    uint32_t off[K];            // b0 + (row0 + q / CH) * row_bytes + DB * (q % CH)
 };
 
 template <int T, int NW>
 __device__ __forceinline__ void mmq_lanes(const MmqArgs &a, const uint8_t *wbase, int row0, int wave, MmqLanes<T, NW> &L) {
     using G = MmqTile<T, NW>;
+    static_assert(G::DB % 4 == 0, "part offsets are dword multiples");
     const int lane = threadIdx.x % WAVE;
     const uint32_t row_bytes = (uint32_t) (a.ncols / 256) * G::SBB;
     const uint32_t b0 = (uint32_t) ((uintptr_t) wbase & 3u);     // 0 except for a 2-byte aligned Q6_K expert
 #pragma unroll
     for (int k = 0; k < MmqLanes<T, NW>::K; ++k) {
         const int q = (wave + NW * k) * WAVE + lane;
-        const uint32_t part = (uint32_t) G::DB * (uint32_t) (q % G::CH);
-        L.row[k] = b0 + (uint32_t) (row0 + q / G::CH) * row_bytes + (G::WIN ? 0u : part);
-        L.part[k] = part;
+        L.off[k] = b0 + (uint32_t) (row0 + q / G::CH) * row_bytes + (uint32_t) G::DB * (uint32_t) (q % G::CH);
     }
 }
 
@@ -256,7 +255,7 @@ __device__ __forceinline__ void mmq_issue(const MmqArgs &a, const uint8_t *wbase
     for (int k = 0; k < MmqLanes<T, NW>::K; ++k) {
         const int i = wave + NW * k;
         if (i >= G::N_INS) break;
-        const uint32_t off = G::WIN ? ((L.row[k] + so) & ~3u) + L.part[k] : L.row[k] + so;
+        const uint32_t off = G::WIN ? (L.off[k] + so) & ~3u : L.off[k] + so;
         lds_void_t *dst = (lds_void_t *) (wl + WAVE * G::DB * i);
         if constexpr (G::DB == 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, dst, 16, off, 0, 0, 0);
         else __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, dst, 4, off, 0, 0, 0);
@@ -606,8 +605,8 @@ __device__ __forceinline__ void mmq_superblock_g16(const uint8_t *wrow_up, const
 }
 
 template <int T, bool GATE, int MAXB>
-__global__ __launch_bounds__(mmq_waves(GATE) * WAVE) void mc_mmq_gemm_kernel(const MmqArgs a) {
-    constexpr int NW = mmq_waves(GATE);
+__global__ __launch_bounds__(mmq_waves(GATE, MAXB) * WAVE) void mc_mmq_gemm_kernel(const MmqArgs a) {
+    constexpr int NW = mmq_waves(GATE, MAXB);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     using G = MmqTile<T, NW>;
     constexpr int N_INS = G::N_INS;
@@ -698,8 +697,8 @@ __global__ __launch_bounds__(mmq_waves(GATE) * WAVE) void mc_mmq_gemm_kernel(con
 
 template <int T, int MAXB>
 static hipError_t launch_mmq_tb(const MmqArgs &a, hipStream_t s) {
-    using GG = MmqTile<T, mmq_waves(true)>;
-    using GP = MmqTile<T, mmq_waves(false)>;
+    using GG = MmqTile<T, mmq_waves(true, MAXB)>;
+    using GP = MmqTile<T, mmq_waves(false, MAXB)>;
     const bool gate = a.w_gate != nullptr;
     const uint32_t stage = gate ? 2u * GG::WT + MAXB * MMQ_REC_BYTES + 1024u : GP::WT + MAXB * MMQ_REC_BYTES + 1024u;
     const int rows = gate ? GG::ROWS : GP::ROWS;
@@ -711,8 +710,8 @@ static hipError_t launch_mmq_tb(const MmqArgs &a, hipStream_t s) {
         hipFuncAttributeMaxDynamicSharedMemorySize, (int) (2 * (GP::WT + MAXB * MMQ_REC_BYTES + 1024u)));
     if (attr_gate != hipSuccess) return attr_gate;
     if (attr_plain != hipSuccess) return attr_plain;
-    if (gate) hipLaunchKernelGGL((mc_mmq_gemm_kernel<T, true, MAXB>), grid, dim3(mmq_waves(true) * WAVE), 2 * stage, s, a);
-    else hipLaunchKernelGGL((mc_mmq_gemm_kernel<T, false, MAXB>), grid, dim3(mmq_waves(false) * WAVE), 2 * stage, s, a);
+    if (gate) hipLaunchKernelGGL((mc_mmq_gemm_kernel<T, true, MAXB>), grid, dim3(mmq_waves(true, MAXB) * WAVE), 2 * stage, s, a);
+    else hipLaunchKernelGGL((mc_mmq_gemm_kernel<T, false, MAXB>), grid, dim3(mmq_waves(false, MAXB) * WAVE), 2 * stage, s, a);
     return hipGetLastError();
 }
 
