@@ -231,12 +231,15 @@ __global__ __launch_bounds__(64) void mc_quantize_q8_K_kernel(const QuantArgs a)
     }
     uint8_t *yb = a.y + row * a.y_stride + b * 292;
     if (amax == 0.0f) {
-        for (int i = 0; i < 4; ++i) yb[4 + 4 * lane + i] = 0;
+        *(u32 *) (yb + 4 + 4 * lane) = 0u;
         if (lane < 8) *(u32 *) (yb + 260 + 4 * lane) = 0u;
         if (lane == 0) *(float *) yb = 0.0f;
         return;
     }
-    const float mx = xb[aidx];
+    // the signed value at aidx, from the lane that holds it (no second read of the row)
+    const int own = aidx & 3;
+    const float mine = own == 0 ? xv[0] : own == 1 ? xv[1] : own == 2 ? xv[2] : xv[3];
+    const float mx = __shfl(mine, aidx >> 2, WAVE);
     const float iscale = -127.0f / mx;
     int qs[4];
 #pragma unroll
@@ -248,8 +251,10 @@ __global__ __launch_bounds__(64) void mc_quantize_q8_K_kernel(const QuantArgs a)
         }
         int v = (int) rintf(p);
         qs[i] = v < 127 ? v : 127;
-        yb[4 + 4 * lane + i] = (uint8_t) (int8_t) qs[i];
     }
+    // the lane's four codes in one 4-byte store (blocks are 292 bytes: 4-byte aligned)
+    *(u32 *) (yb + 4 + 4 * lane) = (u32) (uint8_t) qs[0] | ((u32) (uint8_t) qs[1] << 8) |
+                                   ((u32) (uint8_t) qs[2] << 16) | ((u32) (uint8_t) qs[3] << 24);
     // bsums: 16 values = 4 lanes
     int s = qs[0] + qs[1] + qs[2] + qs[3];
     s += __shfl_xor(s, 1, WAVE);
